@@ -1,0 +1,527 @@
+// C ABI of libattnnn.so: context, buffer layouts, weight packing and the
+// orchestration of a forward (prefill / decode step) over the gfx950 kernels.
+//
+// One forward over M token rows (B sequences x T tokens):
+//   embed_rms                        x = x0 = rms(embed[tok])
+//   per layer l:
+//     proj  RMS -> qkv^T   STORE     qkv = bf16(rms(x) @ [Wq Wk Wv] * sa0)
+//     qkv_post                       q = rope(rms(q)); K/V cache += rope(rms(k)), v
+//     attention (+ combine)          window / full-causal, fp32 softmax
+//     proj  o^T            RESID_ATTN   x = r0 x + p0 (a @ Wo*sa1) + x0l x0
+//     proj  RMS -> fc^T    RELU2     h = relu(rms(x) @ fc)^2
+//     proj  proj^T         RESID_MLP x = r1 x + p1 (h @ proj)
+//   proj RMS -> lm_head^T  LOGITS    z = bf16(rms(x) @ lm_head) (last rows)
+//   sample                           one token per sequence
+// `proj` is the GEMV (M <= 8) or the MFMA GEMM.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <string>
+#include <vector>
+#include "attnnn.h"
+#include "launch.h"
+
+using namespace ann;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                  \
+  do {                                                                                \
+    hipError_t e_ = (expr);                                                           \
+    if (e_ != hipSuccess)                                                             \
+      return fail(ANN_E_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));          \
+  } while (0)
+
+constexpr size_t ALIGN = 256;
+constexpr int MAX_SPLIT = 32;
+
+size_t up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
+
+struct WLayout {  // byte offsets into the packed weight buffer
+  size_t embed, head, layer0, layer_stride, qkv, o, fc, proj, lam, cs, sn, total;
+};
+
+WLayout weight_layout(const ann_config& c) {
+  const size_t d = c.d, V = c.V, Dh = d / c.H;
+  WLayout w{};
+  size_t off = 0;
+  w.embed = off; off += up(V * d * 2);
+  w.head = off; off += up(V * d * 2);
+  w.qkv = 0;
+  w.o = up(3 * d * d * 2);
+  w.fc = w.o + up(d * d * 2);
+  w.proj = w.fc + up(4 * d * d * 2);
+  w.layer_stride = w.proj + up(4 * d * d * 2);
+  w.layer0 = off; off += w.layer_stride * c.L;
+  w.lam = off; off += up((size_t)c.L * 8 * 4);
+  w.cs = off; off += up((size_t)c.max_ctx * (Dh / 4) * 4);
+  w.sn = off; off += up((size_t)c.max_ctx * (Dh / 4) * 4);
+  w.total = off;
+  return w;
+}
+
+struct SLayout {  // byte offsets into the workspace
+  size_t pos, x, x0, qkv, q, ao, hid, rs, part, zb, total;
+};
+
+SLayout ws_layout(const ann_config& c) {
+  const size_t d = c.d, M = c.max_tokens, B = c.max_batch, Dh = d / c.H;
+  SLayout s{};
+  size_t off = 0;
+  s.pos = off; off += up(B * 4);
+  s.x = off; off += up(M * d * 2);
+  s.x0 = off; off += up(M * d * 2);
+  s.qkv = off; off += up(M * 3 * d * 2);
+  s.q = off; off += up(M * d * 2);
+  s.ao = off; off += up(M * d * 2);
+  s.hid = off; off += up(M * 4 * d * 2);
+  s.rs = off; off += up(M * 4);
+  s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
+  s.zb = off; off += up(B * (size_t)c.V * 2);
+  s.total = off;
+  return s;
+}
+
+size_t kv_layer_bytes(const ann_config& c) {
+  return (size_t)c.max_batch * c.max_ctx * c.d * 2;  // B x H x ctx x Dh bf16
+}
+
+int check_config(const ann_config* c) {
+  if (!c) return fail(ANN_E_ARG, "config is null");
+  if (c->d <= 0 || c->L <= 0 || c->H <= 0 || c->V <= 0)
+    return fail(ANN_E_ARG, "d, L, H, V must be positive");
+  if (c->d % c->H) return fail(ANN_E_ARG, "d=%d not divisible by H=%d", c->d, c->H);
+  const int Dh = c->d / c->H;
+  if (Dh != 64 && Dh != 128) return fail(ANN_E_ARG, "head_dim %d unsupported (64 or 128)", Dh);
+  if (c->d % 64) return fail(ANN_E_ARG, "d=%d must be a multiple of 64", c->d);
+  if (c->V_sample <= 0 || c->V_sample > c->V)
+    return fail(ANN_E_ARG, "V_sample=%d outside [1, V=%d]", c->V_sample, c->V);
+  if (c->window <= 0) return fail(ANN_E_ARG, "window must be positive");
+  if (c->n_long < 0 || c->n_long > ANN_MAX_LONG_LAYERS)
+    return fail(ANN_E_ARG, "n_long=%d outside [0, %d]", c->n_long, ANN_MAX_LONG_LAYERS);
+  for (int i = 0; i < c->n_long; ++i)
+    if (c->long_layers[i] < 0 || c->long_layers[i] >= c->L)
+      return fail(ANN_E_ARG, "long layer %d outside [0, %d)", c->long_layers[i], c->L);
+  if (c->max_batch <= 0 || c->max_ctx <= 0 || c->max_tokens <= 0)
+    return fail(ANN_E_ARG, "max_batch, max_ctx, max_tokens must be positive");
+  if (c->max_tokens < c->max_batch)
+    return fail(ANN_E_ARG, "max_tokens=%d < max_batch=%d", c->max_tokens, c->max_batch);
+  if (!(c->rms_eps > 0.f)) return fail(ANN_E_ARG, "rms_eps must be positive");
+  return ANN_OK;
+}
+
+}  // namespace
+
+struct ann_ctx {
+  ann_config c;
+  int Dh;
+  WLayout wl;
+  SLayout sl;
+  uint8_t* w = nullptr;
+  uint8_t* kv = nullptr;
+  uint8_t* ws = nullptr;
+  bool bound = false;
+  int len = 0;  // tokens held per sequence
+  int B = 0;    // sequences held
+  // measurement: HIP event pairs around every launch of one kernel class
+  int prof_kind = -1;
+  std::vector<hipEvent_t> prof_ev;
+  size_t prof_used = 0;
+
+  const bf16_t* wptr(size_t off) const { return (const bf16_t*)(w + off); }
+  const bf16_t* layer_w(int l, size_t off) const {
+    return (const bf16_t*)(w + wl.layer0 + wl.layer_stride * l + off);
+  }
+  bf16_t* kcache(int l) const { return (bf16_t*)(kv + kv_layer_bytes(c) * l); }
+  bf16_t* vcache(int l) const { return (bf16_t*)(kv + kv_layer_bytes(c) * (c.L + l)); }
+  template <typename T> T* sp(size_t off) const { return (T*)(ws + off); }
+  bool is_long(int l) const {
+    for (int i = 0; i < c.n_long; ++i)
+      if (c.long_layers[i] == l) return true;
+    return false;
+  }
+};
+
+namespace {
+
+struct ProfScope {  // records an event pair around a launch of the profiled kind
+  ann_ctx* c;
+  hipStream_t st;
+  bool on;
+  ProfScope(ann_ctx* c_, int kind, hipStream_t st_) : c(c_), st(st_) {
+    on = c->prof_kind == kind && c->prof_used + 2 <= c->prof_ev.size();
+    if (on) hipEventRecord(c->prof_ev[c->prof_used], st);
+  }
+  ~ProfScope() {
+    if (on) {
+      hipEventRecord(c->prof_ev[c->prof_used + 1], st);
+      c->prof_used += 2;
+    }
+  }
+};
+
+// y = (rms?)(X) @ W^T for M rows with the given epilogue.
+int proj(ann_ctx* c, int kind, int epi, bool rms, const bf16_t* W, const bf16_t* X, int ldx,
+         int M, int N, int K, EpiArgs ea, hipStream_t st) {
+  float* rs = nullptr;
+  const bool use_gemv = gemv_fits(M, K);
+  if (rms && !use_gemv) {
+    rs = c->sp<float>(c->sl.rs);
+    HIPCHK(row_rms_scale(X, ldx, rs, M, K, c->c.rms_eps, st));
+  }
+  ProfScope ps(c, kind, st);
+  if (use_gemv)
+    HIPCHK(gemv(epi, rms, W, X, ldx, M, N, K, c->c.rms_eps, ea, st));
+  else
+    HIPCHK(gemm(epi, X, ldx, rs, W, M, N, K, ea, st));
+  return ANN_OK;
+}
+
+// embed + all layers for M = B*T rows whose positions start at pos[b].
+int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
+  const ann_config& g = c->c;
+  const int M = B * T, d = g.d, H = g.H, Dh = c->Dh;
+  bf16_t* x = c->sp<bf16_t>(c->sl.x);
+  bf16_t* x0 = c->sp<bf16_t>(c->sl.x0);
+  bf16_t* qkv = c->sp<bf16_t>(c->sl.qkv);
+  bf16_t* q = c->sp<bf16_t>(c->sl.q);
+  bf16_t* ao = c->sp<bf16_t>(c->sl.ao);
+  bf16_t* hid = c->sp<bf16_t>(c->sl.hid);
+  float* part = c->sp<float>(c->sl.part);
+  const int32_t* pos = c->sp<int32_t>(c->sl.pos);
+  const float* lam = (const float*)(c->w + c->wl.lam);
+  const float* cs = (const float*)(c->w + c->wl.cs);
+  const float* sn = (const float*)(c->w + c->wl.sn);
+
+  HIPCHK(embed_rms(tokens, c->wptr(c->wl.embed), x, x0, M, d, g.V, g.rms_eps, st));
+  for (int l = 0; l < g.L; ++l) {
+    const bool lng = c->is_long(l);
+    EpiArgs ea{};
+    ea.out = qkv;
+    ea.ldo = 3 * d;
+    int rc = proj(c, ANN_PROF_QKV, EPI_STORE, true, c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d, ea, st);
+    if (rc) return rc;
+    HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,
+                    g.rms_eps, st));
+    int nsplit = 1;
+    if (T == 1) {  // decode: split long key ranges so B*H*nsplit fills the GPU
+      const int n = lng ? c->len + 1 : (c->len + 1 < g.window ? c->len + 1 : g.window);
+      const int chunks = (n + 63) / 64;
+      int want = (512 + B * H - 1) / (B * H);
+      nsplit = chunks < want ? chunks : want;
+      if (nsplit > MAX_SPLIT) nsplit = MAX_SPLIT;
+      if (nsplit < 1) nsplit = 1;
+    }
+    {
+      ProfScope ps(c, ANN_PROF_ATTN, st);
+      HIPCHK(attention(q, c->kcache(l), c->vcache(l), pos, ao, part, M, T, H, Dh, g.max_ctx,
+                       g.window, lng, g.attn_scale, nsplit, st));
+    }
+    EpiArgs er{};
+    er.x = x;
+    er.x0 = x0;
+    er.ldr = d;
+    er.lam = lam + 8 * l;
+    rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, false, c->layer_w(l, c->wl.o), ao, d, M, d, d, er, st);
+    if (rc) return rc;
+    EpiArgs eh{};
+    eh.out = hid;
+    eh.ldo = 4 * d;
+    rc = proj(c, ANN_PROF_FC, EPI_RELU2, true, c->layer_w(l, c->wl.fc), x, d, M, 4 * d, d, eh, st);
+    if (rc) return rc;
+    rc = proj(c, ANN_PROF_PROJ, EPI_RESID_MLP, false, c->layer_w(l, c->wl.proj), hid, 4 * d, M, d, 4 * d, er, st);
+    if (rc) return rc;
+  }
+  return ANN_OK;
+}
+
+int check_ready(const ann_ctx* c) {
+  if (!c) return fail(ANN_E_ARG, "context is null");
+  if (!c->bound) return fail(ANN_E_STATE, "buffers not bound (call ann_bind first)");
+  return ANN_OK;
+}
+
+int check_sampling(const ann_ctx* c, const ann_sampling* s) {
+  if (!s) return fail(ANN_E_ARG, "sampling is null");
+  if (!(s->temperature >= 0.f) || s->temperature != s->temperature)
+    return fail(ANN_E_ARG, "temperature must be >= 0");
+  (void)c;
+  return ANN_OK;
+}
+
+// z of the last row of each sequence -> sampled token.
+int head_and_sample(ann_ctx* c, int B, int T, const ann_sampling* s, int32_t* out_tok,
+                    float* logits, hipStream_t st) {
+  const ann_config& g = c->c;
+  bf16_t* x = c->sp<bf16_t>(c->sl.x);
+  bf16_t* zb = c->sp<bf16_t>(c->sl.zb);
+  EpiArgs ez{};
+  ez.z = zb;
+  ez.logits = logits;
+  ez.ldz = g.V;
+  int rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, true, c->wptr(c->wl.head), x + (size_t)(T - 1) * g.d, T * g.d, B,
+                g.V, g.d, ez, st);
+  if (rc) return rc;
+  HIPCHK(sample(zb, g.V, B, g.V_sample, s->temperature, s->top_k, s->seed, s->step, out_tok, st));
+  return ANN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ann_last_error(void) { return g_err.c_str(); }
+int ann_version(void) { return 1; }
+
+int ann_create(const ann_config* cfg, ann_ctx** out) {
+  if (!out) return fail(ANN_E_ARG, "out is null");
+  *out = nullptr;
+  int rc = check_config(cfg);
+  if (rc) return rc;
+  ann_ctx* c = new ann_ctx();
+  c->c = *cfg;
+  c->Dh = cfg->d / cfg->H;
+  c->wl = weight_layout(*cfg);
+  c->sl = ws_layout(*cfg);
+  *out = c;
+  return ANN_OK;
+}
+
+void ann_destroy(ann_ctx* ctx) {
+  if (!ctx) return;
+  for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
+  delete ctx;
+}
+
+int ann_profile_enable(ann_ctx* c, int32_t kind, int32_t max_launches) {
+  if (!c) return fail(ANN_E_ARG, "context is null");
+  if (kind < -1 || kind > ANN_PROF_ATTN) return fail(ANN_E_ARG, "bad kernel kind %d", kind);
+  for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
+  c->prof_ev.clear();
+  c->prof_used = 0;
+  c->prof_kind = -1;
+  if (kind < 0) return ANN_OK;
+  if (max_launches <= 0) return fail(ANN_E_ARG, "max_launches must be positive");
+  c->prof_ev.resize((size_t)max_launches * 2);
+  for (auto& e : c->prof_ev) HIPCHK(hipEventCreate(&e));
+  c->prof_kind = kind;
+  return ANN_OK;
+}
+
+int ann_profile_read(ann_ctx* c, float* total_ms, int32_t* launches) {
+  if (!c || !total_ms || !launches) return fail(ANN_E_ARG, "null argument");
+  double tot = 0.0;
+  for (size_t i = 0; i + 1 < c->prof_used; i += 2) {
+    HIPCHK(hipEventSynchronize(c->prof_ev[i + 1]));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, c->prof_ev[i], c->prof_ev[i + 1]));
+    tot += ms;
+  }
+  *total_ms = (float)tot;
+  *launches = (int32_t)(c->prof_used / 2);
+  c->prof_used = 0;
+  return ANN_OK;
+}
+
+size_t ann_weight_bytes(const ann_config* cfg) {
+  return check_config(cfg) ? 0 : weight_layout(*cfg).total;
+}
+
+size_t ann_kv_bytes(const ann_config* cfg) {
+  return check_config(cfg) ? 0 : kv_layer_bytes(*cfg) * 2 * cfg->L;
+}
+
+size_t ann_workspace_bytes(const ann_config* cfg) {
+  return check_config(cfg) ? 0 : ws_layout(*cfg).total;
+}
+
+int ann_pack_weights(ann_ctx* c, const ann_params_f32* p, void* wbuf, size_t wbytes,
+                     void* stream) {
+  if (!c || !p || !wbuf) return fail(ANN_E_ARG, "null argument");
+  if (wbytes < c->wl.total)
+    return fail(ANN_E_CAPACITY, "weight buffer %zu bytes < required %zu", wbytes, c->wl.total);
+  if (!p->embed || !p->lm_head || !p->attn_bank || !p->fc_bank || !p->proj_bank ||
+      !p->resid_lambdas || !p->post_lambdas || !p->x0_lambdas || !p->sa_lambdas)
+    return fail(ANN_E_ARG, "a parameter pointer is null");
+  hipStream_t st = (hipStream_t)stream;
+  const ann_config& g = c->c;
+  const int d = g.d, V = g.V, L = g.L;
+  uint8_t* w = (uint8_t*)wbuf;
+  HIPCHK(pack_cast(p->embed, (bf16_t*)(w + c->wl.embed), (size_t)V * d, st));
+  HIPCHK(pack_transpose(p->lm_head, (bf16_t*)(w + c->wl.head), d, V, d, nullptr, st));
+  for (int l = 0; l < L; ++l) {
+    uint8_t* lw = w + c->wl.layer0 + c->wl.layer_stride * l;
+    const float* ab = p->attn_bank + (size_t)l * 4 * d * d;
+    for (int j = 0; j < 3; ++j)
+      HIPCHK(pack_transpose(ab + (size_t)j * d * d, (bf16_t*)(lw + c->wl.qkv) + (size_t)j * d * d,
+                            d, d, d, p->sa_lambdas + 2 * l, st));
+    HIPCHK(pack_transpose(ab + (size_t)3 * d * d, (bf16_t*)(lw + c->wl.o), d, d, d,
+                          p->sa_lambdas + 2 * l + 1, st));
+    HIPCHK(pack_transpose(p->fc_bank + (size_t)l * d * 4 * d, (bf16_t*)(lw + c->wl.fc), d, 4 * d,
+                          d, nullptr, st));
+    HIPCHK(pack_transpose(p->proj_bank + (size_t)l * 4 * d * d, (bf16_t*)(lw + c->wl.proj), 4 * d,
+                          d, 4 * d, nullptr, st));
+  }
+  HIPCHK(pack_lambdas(p->resid_lambdas, p->post_lambdas, p->x0_lambdas, (float*)(w + c->wl.lam),
+                      L, st));
+  HIPCHK(rope_tables((float*)(w + c->wl.cs), (float*)(w + c->wl.sn), g.max_ctx, c->Dh,
+                     g.rope_base, st));
+  return ANN_OK;
+}
+
+int ann_bind(ann_ctx* c, void* wbuf, size_t wbytes, void* kv, size_t kvbytes, void* workspace,
+             size_t wsbytes) {
+  if (!c || !wbuf || !kv || !workspace) return fail(ANN_E_ARG, "null argument");
+  if (wbytes < c->wl.total)
+    return fail(ANN_E_CAPACITY, "weight buffer %zu bytes < required %zu", wbytes, c->wl.total);
+  const size_t kvneed = kv_layer_bytes(c->c) * 2 * c->c.L;
+  if (kvbytes < kvneed)
+    return fail(ANN_E_CAPACITY, "kv buffer %zu bytes < required %zu", kvbytes, kvneed);
+  if (wsbytes < c->sl.total)
+    return fail(ANN_E_CAPACITY, "workspace %zu bytes < required %zu", wsbytes, c->sl.total);
+  if (((uintptr_t)wbuf | (uintptr_t)kv | (uintptr_t)workspace) & 255)
+    return fail(ANN_E_ARG, "buffers must be 256-byte aligned");
+  c->w = (uint8_t*)wbuf;
+  c->kv = (uint8_t*)kv;
+  c->ws = (uint8_t*)workspace;
+  c->bound = true;
+  c->len = 0;
+  c->B = 0;
+  return ANN_OK;
+}
+
+int ann_reset(ann_ctx* c) {
+  if (!c) return fail(ANN_E_ARG, "context is null");
+  c->len = 0;
+  c->B = 0;
+  return ANN_OK;
+}
+
+int ann_context_length(const ann_ctx* c) { return c ? c->len : -1; }
+
+static int check_prefill_shape(ann_ctx* c, const int32_t* tokens, int B, int T) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!tokens) return fail(ANN_E_ARG, "tokens is null");
+  if (B < 1 || T < 1) return fail(ANN_E_ARG, "B=%d, T=%d must be >= 1", B, T);
+  if (B > c->c.max_batch) return fail(ANN_E_CAPACITY, "B=%d > max_batch=%d", B, c->c.max_batch);
+  if (T > c->c.max_ctx) return fail(ANN_E_CAPACITY, "T=%d > max_ctx=%d", T, c->c.max_ctx);
+  if ((size_t)B * T > (size_t)c->c.max_tokens)
+    return fail(ANN_E_CAPACITY, "B*T=%d > max_tokens=%d", B * T, c->c.max_tokens);
+  return ANN_OK;
+}
+
+int ann_forward_logits(ann_ctx* c, const int32_t* tokens, int32_t B, int32_t T, float* logits,
+                       void* stream) {
+  int rc = check_prefill_shape(c, tokens, B, T);
+  if (rc) return rc;
+  if (!logits) return fail(ANN_E_ARG, "logits is null");
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* pos = c->sp<int32_t>(c->sl.pos);
+  HIPCHK(set_pos(pos, B, 0, st));
+  c->len = 0;
+  c->B = B;
+  rc = run_body(c, tokens, B, T, st);
+  if (rc) return rc;
+  EpiArgs ez{};
+  ez.logits = logits;
+  ez.ldz = c->c.V;
+  rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, true, c->wptr(c->wl.head), c->sp<bf16_t>(c->sl.x), c->c.d, B * T,
+            c->c.V, c->c.d, ez, st);
+  if (rc) return rc;
+  HIPCHK(advance_pos(pos, B, T, st));
+  c->len = T;
+  return ANN_OK;
+}
+
+int ann_prefill(ann_ctx* c, const int32_t* tokens, int32_t B, int32_t T, const ann_sampling* s,
+                int32_t* out_tok, float* logits, void* stream) {
+  int rc = check_prefill_shape(c, tokens, B, T);
+  if (rc) return rc;
+  rc = check_sampling(c, s);
+  if (rc) return rc;
+  if (!out_tok) return fail(ANN_E_ARG, "out_tok is null");
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* pos = c->sp<int32_t>(c->sl.pos);
+  HIPCHK(set_pos(pos, B, 0, st));
+  c->len = 0;
+  c->B = B;
+  rc = run_body(c, tokens, B, T, st);
+  if (rc) return rc;
+  rc = head_and_sample(c, B, T, s, out_tok, logits, st);
+  if (rc) return rc;
+  HIPCHK(advance_pos(pos, B, T, st));
+  c->len = T;
+  return ANN_OK;
+}
+
+int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_sampling* s,
+                    int32_t* out_tok, float* logits, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  rc = check_sampling(c, s);
+  if (rc) return rc;
+  if (!tokens || !out_tok) return fail(ANN_E_ARG, "tokens / out_tok is null");
+  if (c->len == 0) return fail(ANN_E_STATE, "no sequences: prefill first");
+  if (B != c->B) return fail(ANN_E_ARG, "B=%d differs from the prefilled batch %d", B, c->B);
+  if (c->len + 1 > c->c.max_ctx)
+    return fail(ANN_E_CAPACITY, "context %d would exceed max_ctx=%d", c->len + 1, c->c.max_ctx);
+  hipStream_t st = (hipStream_t)stream;
+  rc = run_body(c, tokens, B, 1, st);
+  if (rc) return rc;
+  rc = head_and_sample(c, B, 1, s, out_tok, logits, st);
+  if (rc) return rc;
+  HIPCHK(advance_pos(c->sp<int32_t>(c->sl.pos), B, 1, st));
+  c->len += 1;
+  return ANN_OK;
+}
+
+int ann_op_relu2(const void* x, void* y, size_t n, int32_t dtype, void* stream) {
+  if ((!x || !y) && n) return fail(ANN_E_ARG, "null argument");
+  if (dtype != ANN_DTYPE_F32 && dtype != ANN_DTYPE_BF16) return fail(ANN_E_ARG, "bad dtype");
+  HIPCHK(op_relu2(x, y, n, dtype, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+int ann_op_rope_ht(const void* x, void* y, const float* cs, const float* sn, int32_t B, int32_t T,
+                   int32_t H, int32_t D, int32_t pos0, int32_t inverse, int32_t dtype,
+                   void* stream) {
+  if (!x || !y || !cs || !sn) return fail(ANN_E_ARG, "null argument");
+  if (B < 0 || T < 0 || H < 0 || D <= 0 || D % 4 || pos0 < 0)
+    return fail(ANN_E_ARG, "bad shape B=%d T=%d H=%d D=%d pos0=%d", B, T, H, D, pos0);
+  if (dtype != ANN_DTYPE_F32 && dtype != ANN_DTYPE_BF16) return fail(ANN_E_ARG, "bad dtype");
+  HIPCHK(op_rope(x, y, cs, sn, B, T, H, D, pos0, inverse, dtype, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+int ann_op_rope_tables(float* cs, float* sn, int32_t seq_len, int32_t head_dim, float base,
+                       void* stream) {
+  if (!cs || !sn) return fail(ANN_E_ARG, "null argument");
+  if (seq_len <= 0 || head_dim <= 0 || head_dim % 4 || !(base > 0.f))
+    return fail(ANN_E_ARG, "bad table shape");
+  HIPCHK(rope_tables(cs, sn, seq_len, head_dim, base, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+int ann_op_rms_norm(const void* x, void* y, int32_t rows, int32_t dim, float eps, int32_t dtype,
+                    void* stream) {
+  if (!x || !y) return fail(ANN_E_ARG, "null argument");
+  if (rows < 0 || dim <= 0) return fail(ANN_E_ARG, "bad shape rows=%d dim=%d", rows, dim);
+  if (dtype != ANN_DTYPE_F32 && dtype != ANN_DTYPE_BF16) return fail(ANN_E_ARG, "bad dtype");
+  HIPCHK(op_rms(x, y, rows, dim, eps, dtype, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,318 @@
+// Element-wise and row kernels: weight packing, RoPE tables, embedding +
+// RMSNorm, QK-norm + RoPE + KV-cache append, and the operator entry points
+// (relu2, rope_ht, rms_norm) that mirror the reference's Metal kernels.
+#include "common.h"
+#include "launch.h"
+
+namespace ann {
+
+// ---- weight packing ---------------------------------------------------------
+
+// dst (N, K) bf16 row-major  <-  src (K, N) fp32 row-major (the reference's
+// (in, out) storage), value bf16(bf16(w) * bf16(scale)) when scale_ptr is set
+// (model.py:239-241: weights cast to bf16, then multiplied by a bf16 lambda),
+// plain bf16(w) otherwise.  32x32 tiles through LDS so both sides coalesce.
+__global__ void k_pack_transpose(const float* __restrict__ src, bf16_t* __restrict__ dst,
+                                 int K, int N, int ldd, const float* __restrict__ scale_ptr) {
+  __shared__ float tile[32][33];
+  const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    int k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < K && n < N) ? src[(size_t)k * N + n] : 0.f;
+  }
+  __syncthreads();
+  const float s = scale_ptr ? rbf(*scale_ptr) : 1.f;
+  for (int r = ty; r < 32; r += 8) {
+    int n = n0 + r, k = k0 + tx;
+    if (n < N && k < K) {
+      float w = rbf(tile[tx][r]);
+      dst[(size_t)n * ldd + k] = f2bf(scale_ptr ? w * s : w);
+    }
+  }
+}
+
+// Same-layout fp32 -> bf16 copy (embedding rows).
+__global__ void k_pack_cast(const float* __restrict__ src, bf16_t* __restrict__ dst, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = f2bf(src[i]);
+}
+
+// Per-layer lambdas, bf16-rounded (model.py:229-232): row l = r0 r1 p0 p1 x0.
+__global__ void k_pack_lambdas(const float* resid, const float* post, const float* x0l,
+                               float* out, int L) {
+  int l = blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= L) return;
+  float* o = out + l * 8;
+  o[0] = rbf(resid[2 * l]);
+  o[1] = rbf(resid[2 * l + 1]);
+  o[2] = rbf(post[2 * l]);
+  o[3] = rbf(post[2 * l + 1]);
+  o[4] = rbf(x0l[l]);
+  o[5] = o[6] = o[7] = 0.f;
+}
+
+// RoPE tables (metal_kernels.py:144-150): freq_i = (1/base)^(i/(D/4-1)),
+// theta = t * freq_i, fp32 cos / sin.
+__global__ void k_rope_tables(float* cs, float* sn, int seq_len, int d4, float base) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= seq_len * d4) return;
+  int t = i / d4, j = i % d4;
+  float lin = d4 > 1 ? (float)j / (float)(d4 - 1) : 0.f;
+  float freq = powf(1.0f / base, lin);
+  float th = (float)t * freq;
+  cs[i] = cosf(th);
+  sn[i] = sinf(th);
+}
+
+// ---- embedding + RMSNorm ------------------------------------------------------
+
+// x = x0 = rms(bf16(embed[tok])) (model.py:236-237).  One block per row.
+__global__ void k_embed_rms(const int32_t* __restrict__ tok, const bf16_t* __restrict__ emb,
+                            bf16_t* __restrict__ x, bf16_t* __restrict__ x0, int d, int V,
+                            float eps) {
+  __shared__ float red[16];
+  const int m = blockIdx.x;
+  int t = tok[m];
+  t = t < 0 ? 0 : (t >= V ? V - 1 : t);   // host validates; clamp keeps reads in bounds
+  const bf16_t* e = emb + (size_t)t * d;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    float v = bf2f(e[i]);
+    ss += v * v;
+  }
+  float s = rsqrtf(block_sum(ss, red) / (float)d + eps);
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    bf16_t r = f2bf(bf2f(e[i]) * s);
+    x[(size_t)m * d + i] = r;
+    x0[(size_t)m * d + i] = r;
+  }
+}
+
+// Row scale s_m = rsqrt(mean(x_m^2) + eps) for the GEMM RMS prologue.
+__global__ void k_row_rms_scale(const bf16_t* __restrict__ x, int ldx, float* __restrict__ s,
+                                int M, int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const bf16_t* r = x + (size_t)m * ldx;
+  float ss = 0.f;
+  for (int i = lane; i < d; i += 64) {
+    float v = bf2f(r[i]);
+    ss += v * v;
+  }
+  ss = group_sum<64>(ss);
+  if (lane == 0) s[m] = rsqrtf(ss / (float)d + eps);
+}
+
+// ---- QK-norm + RoPE + KV-cache append --------------------------------------
+
+// qkv (M, 3*H*Dh) bf16 -> q (M, H*Dh) = rope(rms(q)); K/V cache rows written
+// at the token's position (model.py:244-247).  Row m is token t = m % T of
+// sequence b = m / T at position pos[b] + t.  Cache layout [b][h][ctx][Dh].
+// One group of Dh/2 lanes per (row, head); each lane owns one dim pair.
+template <int DH>
+__global__ void k_qkv_post(const bf16_t* __restrict__ qkv, bf16_t* __restrict__ q,
+                           bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+                           const int32_t* __restrict__ pos, const float* __restrict__ cs,
+                           const float* __restrict__ sn, int M, int T, int H, int max_ctx,
+                           float eps) {
+  constexpr int P = DH / 2;                  // lanes per head
+  constexpr int D4 = DH / 4;
+  const int gid = blockIdx.x * (blockDim.x / P) + threadIdx.x / P;
+  const int p = threadIdx.x % P;
+  if (gid >= M * H) return;
+  const int m = gid / H, h = gid % H;
+  const int b = m / T, t = m % T;
+  const int ps = pos[b] + t;
+  const int d = H * DH;
+  const bf16_t* row = qkv + (size_t)m * 3 * d;
+  const uint32_t qw = *(const uint32_t*)(row + h * DH + 2 * p);
+  const uint32_t kw = *(const uint32_t*)(row + d + h * DH + 2 * p);
+  const uint32_t vw = *(const uint32_t*)(row + 2 * d + h * DH + 2 * p);
+  float q0 = __uint_as_float(qw << 16), q1 = __uint_as_float(qw & 0xffff0000u);
+  float k0 = __uint_as_float(kw << 16), k1 = __uint_as_float(kw & 0xffff0000u);
+  float sq = group_sum<P>(q0 * q0 + q1 * q1);
+  float sk = group_sum<P>(k0 * k0 + k1 * k1);
+  float rq = rsqrtf(sq / (float)DH + eps), rk = rsqrtf(sk / (float)DH + eps);
+  q0 = rbf(q0 * rq); q1 = rbf(q1 * rq);
+  k0 = rbf(k0 * rk); k1 = rbf(k1 * rk);
+  if (p < D4) {
+    const float c = cs[ps * D4 + p], s = sn[ps * D4 + p];
+    float a0 = c * q0 + s * q1, a1 = c * q1 - s * q0;
+    float b0 = c * k0 + s * k1, b1 = c * k1 - s * k0;
+    q0 = a0; q1 = a1; k0 = b0; k1 = b1;
+  }
+  *(uint32_t*)(q + (size_t)m * d + h * DH + 2 * p) = pack2(q0, q1);
+  const size_t cidx = (((size_t)b * H + h) * max_ctx + ps) * DH + 2 * p;
+  *(uint32_t*)(kc + cidx) = pack2(k0, k1);
+  *(uint32_t*)(vc + cidx) = vw;
+}
+
+// ---- operators (reference kernel API) ----------------------------------------
+
+template <typename T> __device__ __forceinline__ float ldf(const T* p, size_t i);
+template <> __device__ __forceinline__ float ldf<float>(const float* p, size_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ldf<bf16_t>(const bf16_t* p, size_t i) { return bf2f(p[i]); }
+template <typename T> __device__ __forceinline__ void stf(T* p, size_t i, float v);
+template <> __device__ __forceinline__ void stf<float>(float* p, size_t i, float v) { p[i] = v; }
+template <> __device__ __forceinline__ void stf<bf16_t>(bf16_t* p, size_t i, float v) { p[i] = f2bf(v); }
+
+// relu2 (metal_kernels.py:37-47): y = (T)(max(x,0)^2), fp32 inside.
+template <typename T>
+__global__ void k_relu2(const T* __restrict__ x, T* __restrict__ y, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    float v = ldf(x, i);
+    float r = v > 0.f ? v : 0.f;
+    stf(y, i, r * r);
+  }
+}
+
+// rope_ht (metal_kernels.py:87-113), one thread per dim pair, explicit pos0.
+template <typename T>
+__global__ void k_rope(const T* __restrict__ x, T* __restrict__ y, const float* __restrict__ cs,
+                       const float* __restrict__ sn, int B, int Tn, int H, int D, int pos0,
+                       int inverse) {
+  const size_t n = (size_t)B * Tn * H * (D / 2);
+  size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const int D2 = D / 2, D4 = D / 4;
+  size_t row = p / ((size_t)H * D2);
+  int rem = (int)(p % ((size_t)H * D2));
+  int h = rem / D2, d2 = rem % D2;
+  int t = (int)(row % Tn) + pos0;
+  size_t base = row * (size_t)(H * D) + (size_t)h * D + 2 * d2;
+  float x0 = ldf(x, base), x1 = ldf(x, base + 1);
+  if (d2 < D4) {
+    float c = cs[(size_t)t * D4 + d2], s = sn[(size_t)t * D4 + d2];
+    if (inverse) {
+      stf(y, base, c * x0 - s * x1);
+      stf(y, base + 1, c * x1 + s * x0);
+    } else {
+      stf(y, base, c * x0 + s * x1);
+      stf(y, base + 1, c * x1 - s * x0);
+    }
+  } else {
+    stf(y, base, x0);
+    stf(y, base + 1, x1);
+  }
+}
+
+// rms (model.py:48-49) over rows; one block per row.
+template <typename T>
+__global__ void k_rms(const T* __restrict__ x, T* __restrict__ y, int dim, float eps) {
+  __shared__ float red[16];
+  const T* r = x + (size_t)blockIdx.x * dim;
+  T* o = y + (size_t)blockIdx.x * dim;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+    float v = ldf(r, i);
+    ss += v * v;
+  }
+  float s = rsqrtf(block_sum(ss, red) / (float)dim + eps);
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) stf(o, i, ldf(r, i) * s);
+}
+
+// ---- launchers ---------------------------------------------------------------
+
+static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+hipError_t pack_transpose(const float* src, bf16_t* dst, int K, int N, int ldd,
+                          const float* scale, hipStream_t st) {
+  dim3 g(cdiv(N, 32), cdiv(K, 32));
+  hipLaunchKernelGGL(k_pack_transpose, g, dim3(256), 0, st, src, dst, K, N, ldd, scale);
+  return hipGetLastError();
+}
+
+hipError_t pack_cast(const float* src, bf16_t* dst, size_t n, hipStream_t st) {
+  unsigned g = cdiv(n, 256);
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(k_pack_cast, dim3(g), dim3(256), 0, st, src, dst, n);
+  return hipGetLastError();
+}
+
+hipError_t pack_lambdas(const float* resid, const float* post, const float* x0l, float* out,
+                        int L, hipStream_t st) {
+  hipLaunchKernelGGL(k_pack_lambdas, dim3(cdiv(L, 64)), dim3(64), 0, st, resid, post, x0l, out, L);
+  return hipGetLastError();
+}
+
+hipError_t rope_tables(float* cs, float* sn, int seq_len, int head_dim, float base,
+                       hipStream_t st) {
+  int d4 = head_dim / 4;
+  hipLaunchKernelGGL(k_rope_tables, dim3(cdiv((size_t)seq_len * d4, 256)), dim3(256), 0, st, cs,
+                     sn, seq_len, d4, base);
+  return hipGetLastError();
+}
+
+hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x0, int M, int d,
+                     int V, float eps, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed_rms, dim3(M), dim3(256), 0, st, tok, emb, x, x0, d, V, eps);
+  return hipGetLastError();
+}
+
+hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
+                         hipStream_t st) {
+  hipLaunchKernelGGL(k_row_rms_scale, dim3(cdiv(M, 4)), dim3(256), 0, st, x, ldx, s, M, d, eps);
+  return hipGetLastError();
+}
+
+hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const int32_t* pos,
+                    const float* cs, const float* sn, int M, int T, int H, int Dh, int max_ctx,
+                    float eps, hipStream_t st) {
+  const size_t groups = (size_t)M * H;
+  switch (Dh) {
+#define ANN_QKV_CASE(D)                                                                        \
+  case D: {                                                                                    \
+    constexpr int per = 256 / (D / 2);                                                         \
+    hipLaunchKernelGGL(k_qkv_post<D>, dim3(cdiv(groups, per)), dim3(256), 0, st, qkv, q, kc,   \
+                       vc, pos, cs, sn, M, T, H, max_ctx, eps);                                \
+    break;                                                                                     \
+  }
+    ANN_QKV_CASE(32)
+    ANN_QKV_CASE(64)
+    ANN_QKV_CASE(128)
+#undef ANN_QKV_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st) {
+  unsigned g = cdiv(n, 256);
+  if (g > 65536) g = 65536;
+  if (g == 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(k_relu2<float>, dim3(g), dim3(256), 0, st, (const float*)x, (float*)y, n);
+  else
+    hipLaunchKernelGGL(k_relu2<bf16_t>, dim3(g), dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)y, n);
+  return hipGetLastError();
+}
+
+hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,
+                   int D, int pos0, int inverse, int dtype, hipStream_t st) {
+  size_t n = (size_t)B * T * H * (D / 2);
+  if (n == 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(k_rope<float>, dim3(cdiv(n, 256)), dim3(256), 0, st, (const float*)x,
+                       (float*)y, cs, sn, B, T, H, D, pos0, inverse);
+  else
+    hipLaunchKernelGGL(k_rope<bf16_t>, dim3(cdiv(n, 256)), dim3(256), 0, st, (const bf16_t*)x,
+                       (bf16_t*)y, cs, sn, B, T, H, D, pos0, inverse);
+  return hipGetLastError();
+}
+
+hipError_t op_rms(const void* x, void* y, int rows, int dim, float eps, int dtype, hipStream_t st) {
+  if (rows == 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(k_rms<float>, dim3(rows), dim3(256), 0, st, (const float*)x, (float*)y, dim, eps);
+  else
+    hipLaunchKernelGGL(k_rms<bf16_t>, dim3(rows), dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)y, dim, eps);
+  return hipGetLastError();
+}
+
+}  // namespace ann

@@ -1,0 +1,71 @@
+// Host-side launchers of the gfx950 kernels (internal to libattnnn.so).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "common.h"
+
+namespace ann {
+
+// Epilogue of a projection y = a @ W^T (W stored (N, K)):
+//   EPI_STORE       out = bf16(y)
+//   EPI_RELU2       out = bf16(max(bf16(y), 0)^2)                 (model.py:258)
+//   EPI_RESID_ATTN  x = ((r0*x) + (p0*bf16(y))) + (x0l*x0), each op
+//                   rounded to bf16                               (model.py:255-256)
+//   EPI_RESID_MLP   x = (r1*x) + (p1*bf16(y)), each op rounded     (model.py:259-260)
+//   EPI_LOGITS      z = bf16(y) -> zbuf (if set); softcap(z) -> logits fp32 (if set)
+enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4 };
+
+struct EpiArgs {
+  bf16_t* out;       // STORE / RELU2 output (M, ldo)
+  int ldo;
+  bf16_t* x;         // residual stream (M, ldr), updated in place
+  const bf16_t* x0;  // x0 (M, ldr)
+  int ldr;
+  const float* lam;  // this layer's lambda row: r0 r1 p0 p1 x0l
+  bf16_t* z;         // LOGITS: bf16 z (M, ldz) or null
+  float* logits;     // LOGITS: fp32 softcapped (M, ldz) or null
+  int ldz;
+};
+
+hipError_t pack_transpose(const float* src, bf16_t* dst, int K, int N, int ldd,
+                          const float* scale, hipStream_t st);
+hipError_t pack_cast(const float* src, bf16_t* dst, size_t n, hipStream_t st);
+hipError_t pack_lambdas(const float* resid, const float* post, const float* x0l, float* out,
+                        int L, hipStream_t st);
+hipError_t rope_tables(float* cs, float* sn, int seq_len, int head_dim, float base,
+                       hipStream_t st);
+hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x0, int M, int d,
+                     int V, float eps, hipStream_t st);
+hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
+                         hipStream_t st);
+hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const int32_t* pos,
+                    const float* cs, const float* sn, int M, int T, int H, int Dh, int max_ctx,
+                    float eps, hipStream_t st);
+
+// GEMV for M <= 8 rows: y = (rms?)(X) @ W^T, X (M, ldx) bf16.
+hipError_t gemv(int epi, bool rms_in, const bf16_t* W, const bf16_t* X, int ldx, int M, int N,
+                int K, float eps, const EpiArgs& ea, hipStream_t st);
+bool gemv_fits(int M, int K);
+// MFMA GEMM: y = (rs_m * A) @ W^T with A (M, lda) bf16; rs null = no scaling.
+hipError_t gemm(int epi, const bf16_t* A, int lda, const float* rs, const bf16_t* W, int M,
+                int N, int K, const EpiArgs& ea, hipStream_t st);
+
+// Attention of M query rows (row m = token t = m % T of sequence b = m / T at
+// position pos[b] + t) against the KV cache.  nsplit > 1 splits each row's key
+// range over work-groups (flash-decoding) and merges them in a second kernel.
+hipError_t attention(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const int32_t* pos,
+                     bf16_t* out, float* part, int M, int T, int H, int Dh, int max_ctx,
+                     int window, bool long_layer, float scale, int nsplit, hipStream_t st);
+
+// Sampling of B rows of bf16 z (B, ldz) over the first Vs entries.
+hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, float temperature, int top_k,
+                  uint64_t seed, uint64_t step, int32_t* out_tok, hipStream_t st);
+hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st);
+hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st);
+
+hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st);
+hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,
+                   int D, int pos0, int inverse, int dtype, hipStream_t st);
+hipError_t op_rms(const void* x, void* y, int rows, int dim, float eps, int dtype, hipStream_t st);
+
+}  // namespace ann

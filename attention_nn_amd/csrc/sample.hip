@@ -1,0 +1,229 @@
+// Sampling of one token per row from bf16 z = lm_head logits before the
+// softcap (sample.py:44-49):
+//   greedy (temperature 0): argmax of z over the first Vs entries, lowest
+//     index on ties (softcap is increasing, so this is the argmax of the
+//     softcapped logits);
+//   otherwise: zc = softcap(z) / temperature; kth = k-th largest zc; keep
+//     every zc >= kth (ties included, as `where(z < kth, -1e9, z)`); draw
+//     u ~ U[0,1) from Philox4x32-10 and return the first kept index whose
+//     running sum of exp(zc - max) exceeds u * total.
+// The k-th largest is found by a two-pass radix select on the 16-bit ordered
+// keys of z in LDS histograms; one work-group per row.
+#include <math.h>
+#include "common.h"
+#include "launch.h"
+
+namespace ann {
+
+constexpr int SMP_THREADS = 1024;
+
+__device__ __forceinline__ uint32_t okey(bf16_t h) {  // order-preserving 16-bit key
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
+}
+
+__device__ __forceinline__ uint32_t mulhilo(uint32_t a, uint32_t b, uint32_t* hi) {
+  const uint64_t p = (uint64_t)a * b;
+  *hi = (uint32_t)(p >> 32);
+  return (uint32_t)p;
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): first output word.
+__device__ uint32_t philox_x(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                             uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint32_t hi0, hi1;
+    const uint32_t lo0 = mulhilo(0xD2511F53u, c0, &hi0);
+    const uint32_t lo1 = mulhilo(0xCD9E8D57u, c2, &hi1);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    const uint64_t w = ((uint64_t)hi << 32) | lo;
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Largest bin b with count(bins >= b) >= need (bins scanned from the top).
+__device__ int select_bin(const uint32_t* hist, uint32_t need, uint32_t* above) {
+  uint32_t acc = 0;
+  for (int bn = 255; bn >= 0; --bn) {
+    if (acc + hist[bn] >= need) {
+      *above = acc;
+      return bn;
+    }
+    acc += hist[bn];
+  }
+  *above = acc;
+  return 0;
+}
+
+__global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
+                                                        int Vs, float temperature, int top_k,
+                                                        uint64_t seed, uint64_t step,
+                                                        int32_t* __restrict__ out_tok) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t s_red[SMP_THREADS / 64];
+  __shared__ float s_sum[SMP_THREADS];
+  __shared__ uint32_t s_misc[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const bf16_t* z = zall + (size_t)row * ldz;
+
+  if (temperature == 0.f) {
+    uint64_t best = 0;
+    for (int i = tid; i < Vs; i += SMP_THREADS) {
+      const uint64_t key = ((uint64_t)okey(z[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+      best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) s_red[wv] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t b = 0;
+      for (int w = 0; w < SMP_THREADS / 64; ++w) b = s_red[w] > b ? s_red[w] : b;
+      out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+    }
+    return;
+  }
+
+  // ---- k-th largest 16-bit key (exact), or the minimum when keeping all
+  uint32_t thr_key = 0;
+  const bool use_thr = top_k > 0 && top_k < Vs;
+  if (use_thr) {
+    for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < Vs; i += SMP_THREADS) atomicAdd(&hist[okey(z[i]) >> 8], 1u);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t above;
+      const int b1 = select_bin(hist, (uint32_t)top_k, &above);
+      s_misc[0] = (uint32_t)b1;
+      s_misc[1] = (uint32_t)top_k - above;
+    }
+    __syncthreads();
+    const uint32_t b1 = s_misc[0];
+    for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < Vs; i += SMP_THREADS) {
+      const uint32_t k = okey(z[i]);
+      if ((k >> 8) == b1) atomicAdd(&hist[k & 0xffu], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t above;
+      const int b2 = select_bin(hist, s_misc[1], &above);
+      s_misc[2] = (b1 << 8) | (uint32_t)b2;
+    }
+    __syncthreads();
+    thr_key = s_misc[2];
+  }
+
+  // ---- threshold and maximum in the softcapped / tempered domain
+  uint32_t kmax = 0;
+  for (int i = tid; i < Vs; i += SMP_THREADS) kmax = max(kmax, okey(z[i]));
+  {
+    uint64_t v = wave_max_u64(kmax);
+    if (lane == 0) s_red[wv] = v;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t b = 0;
+      for (int w = 0; w < SMP_THREADS / 64; ++w) b = s_red[w] > b ? s_red[w] : b;
+      s_misc[3] = (uint32_t)b;
+    }
+    __syncthreads();
+    kmax = s_misc[3];
+  }
+  auto key2bf = [](uint32_t k) -> bf16_t {
+    return (bf16_t)((k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu));
+  };
+  const float tmp = temperature;
+  const float zmax = softcap(bf2f(key2bf(kmax))) / tmp;
+  const float zthr = use_thr ? softcap(bf2f(key2bf(thr_key))) / tmp : -INFINITY;
+
+  // ---- contiguous segment per thread, deterministic scan
+  const int seg = (Vs + SMP_THREADS - 1) / SMP_THREADS;
+  const int i0 = min(Vs, tid * seg), i1 = min(Vs, i0 + seg);
+  float local = 0.f;
+  for (int i = i0; i < i1; ++i) {
+    const float zc = softcap(bf2f(z[i])) / tmp;
+    if (zc >= zthr) local += expf(zc - zmax);
+  }
+  s_sum[tid] = local;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over SMP_THREADS values (fixed order)
+  for (int off = 1; off < SMP_THREADS; off <<= 1) {
+    const float v = tid >= off ? s_sum[tid - off] : 0.f;
+    __syncthreads();
+    s_sum[tid] += v;
+    __syncthreads();
+  }
+  const float total = s_sum[SMP_THREADS - 1];
+  const float before = tid ? s_sum[tid - 1] : 0.f;
+  const uint32_t w = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
+                              (uint32_t)seed, (uint32_t)(seed >> 32));
+  const float target = (float)(w >> 8) * (1.0f / 16777216.0f) * total;
+  if (tid == 0) s_misc[0] = 0xffffffffu;
+  __syncthreads();
+  if (target >= before && target < before + local) {
+    float run = before;
+    int pick = -1, last = -1;
+    for (int i = i0; i < i1; ++i) {
+      const float zc = softcap(bf2f(z[i])) / tmp;
+      if (zc >= zthr) {
+        last = i;
+        run += expf(zc - zmax);
+        if (target < run) { pick = i; break; }
+      }
+    }
+    if (pick < 0) pick = last;
+    atomicMin(&s_misc[0], (uint32_t)pick);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t pick = s_misc[0];
+    if (pick == 0xffffffffu) {  // rounding put target at/after the total: last kept index
+      for (int i = Vs - 1; i >= 0; --i)
+        if (softcap(bf2f(z[i])) / tmp >= zthr) { pick = (uint32_t)i; break; }
+    }
+    out_tok[row] = (int32_t)pick;
+  }
+}
+
+__global__ void k_set_pos(int32_t* pos, int B, int value) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < B) pos[i] = value;
+}
+
+__global__ void k_advance_pos(int32_t* pos, int B, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < B) pos[i] += n;
+}
+
+hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, float temperature, int top_k,
+                  uint64_t seed, uint64_t step, int32_t* out_tok, hipStream_t st) {
+  hipLaunchKernelGGL(k_sample, dim3(B), dim3(SMP_THREADS), 0, st, z, ldz, Vs, temperature, top_k,
+                     seed, step, out_tok);
+  return hipGetLastError();
+}
+
+hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st) {
+  hipLaunchKernelGGL(k_set_pos, dim3((B + 255) / 256), dim3(256), 0, st, pos, B, value);
+  return hipGetLastError();
+}
+
+hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st) {
+  hipLaunchKernelGGL(k_advance_pos, dim3((B + 255) / 256), dim3(256), 0, st, pos, B, n);
+  return hipGetLastError();
+}
+
+}  // namespace ann

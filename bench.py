@@ -1,0 +1,235 @@
+"""Decode benchmark of the token loop on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
+
+Workload: 155M model (d768, 11 layers, 6 heads x
+128, long layers {4,10}, window 384, vocab 50304), random-init bf16 weights
+(model.py distributions, Wo/proj drawn dense), batch 1, 32-token random
+prompt, greedy decode to context 1024: a "step" is one decode step of the
+whole model for the batch.  K steps (default 992 = positions 32..1023) are
+timed with HIP events on the stream the kernels run on, after W warm-up steps
+and a fresh prefill.  value = decoded tokens / s.
+
+roofline: the dominant kernel of the step (the lm_head projection fused
+with the softcap, 2*d*V weight bytes per launch) -- its launches inside the
+timed region are bracketed by HIP event pairs; achieved = algorithmic bytes
+per launch / mean launch time, against the 8 TB/s HBM peak.
+
+secondary: the whole decode step against the HBM roofline, batch-64 decode
+(configs[2]: 512-token prompts, temperature 0.8, top-k 50) and its prefill
+against the bf16 MFMA peak.
+
+cpu_baseline: the CPU oracle (PyTorch restatement of model.py's forward)
+with sample.py's semantics -- a full forward over the whole context for every
+token -- timed at 8 context lengths spanning 32..1023 and integrated over the
+loop; threads = the host cores this process may use.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0
+METRIC = "decode tok/s (155M, batch 1 & 64) + % of HBM/MFMA roofline on 1 MI355X"
+
+
+def step_bytes(cfg, B, pos):
+    """Algorithmic HBM bytes of one decode step at position pos (0-based)."""
+    d, L, V = cfg.model_dim, cfg.num_layers, cfg.vocab_size
+    w = 2 * (12 * d * d * L + d * V)
+    kv = 0
+    for l in range(L):
+        n = pos + 1 if l in cfg.long_layers else min(pos + 1, cfg.window)
+        kv += 4 * d * n
+    return w + B * kv + B * L * 4 * d + B * 2 * d
+
+
+def step_flops(cfg, B, pos):
+    d, L, V = cfg.model_dim, cfg.num_layers, cfg.vocab_size
+    f = 2 * (12 * d * d * L + d * V)
+    for l in range(L):
+        n = pos + 1 if l in cfg.long_layers else min(pos + 1, cfg.window)
+        f += 4 * d * n
+    return B * f
+
+
+def prefill_flops(cfg, B, T):
+    d, L, V = cfg.model_dim, cfg.num_layers, cfg.vocab_size
+    f = 2 * 12 * d * d * L * B * T + 2 * d * V * B
+    for l in range(L):
+        for i in range(T):
+            n = i + 1 if l in cfg.long_layers else min(i + 1, cfg.window)
+            f += B * 4 * d * n
+    return f
+
+
+def lm_head_bytes(cfg, B):
+    d, V = cfg.model_dim, cfg.vocab_size
+    return 2 * d * V + 2 * B * d + 2 * B * V
+
+
+def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=True):
+    import torch
+    B = prompt.shape[0]
+    if warmup:
+        nxt, _ = eng.prefill(prompt, temperature, top_k, seed, 0)
+        for i in range(warmup):
+            nxt, _ = eng.decode(nxt, temperature, top_k, seed, i + 1, out=nxt)
+    torch.cuda.synchronize()
+    nxt, _ = eng.prefill(prompt, temperature, top_k, seed, 0)
+    torch.cuda.synchronize()
+    if prof:
+        eng.profile("lm_head", max_launches=steps + 8)
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for i in range(steps):
+        nxt, _ = eng.decode(nxt, temperature, top_k, seed, i + 1, out=nxt)
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+    head = eng.profile_read() if prof else (0.0, 0)
+    eng.profile(None)
+    return ms, wall, head, B * steps
+
+
+def cpu_baseline(cfg, params, prompt_len, ctx_end, budget_s=20.0):
+    """sample.py semantics on the CPU oracle: full recompute per token."""
+    import torch
+    import oracle.ref_model as R
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    prep = R.Prepared(cfg, params)
+    rng = np.random.default_rng(1)
+    ctxs = np.linspace(prompt_len, ctx_end, 8).astype(int)
+    times = []
+    t_start = time.perf_counter()
+    for T in ctxs:
+        tok = rng.integers(0, 50257, (1, int(T)))
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            R.forward(prep, tok)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    ctxs = ctxs[:len(times)]
+    # per-step time as a function of context, integrated over every step
+    all_ctx = np.arange(prompt_len, ctx_end)
+    per_step = np.interp(all_ctx, ctxs, times)
+    total = float(per_step.sum())
+    return {
+        "value": round(len(all_ctx) / total, 3),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle full-recompute forward (sample.py semantics, no KV cache) timed once "
+                   f"at contexts {list(map(int, ctxs))}, interpolated and summed over the "
+                   f"{len(all_ctx)} steps {prompt_len}..{ctx_end - 1} ({sum(times):.1f} s of CPU work)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=992)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the decode path runs on a single MI355X "
+              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+        return 2
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from attention_nn_amd.config import cfg_155m
+    from attention_nn_amd.engine import Engine
+    from attention_nn_amd.weights import init_params
+
+    torch.cuda.set_device(0)
+    cfg = cfg_155m(seq_len=1024)
+    params = init_params(cfg, seed=0, dense=True)
+    prompt_len = 32
+    steps = min(args.steps, 1024 - prompt_len)
+    prompt = np.random.default_rng(0).integers(0, 50257, (1, prompt_len))
+    eng = Engine(cfg, params, max_batch=1, max_ctx=1024, max_tokens=1024)
+    ms, wall, (head_ms, head_n), toks = run_decode(eng, prompt, steps, args.warmup, 0.0, 0, 0)
+    value = toks / (ms / 1e3)
+    avg_bytes = np.mean([step_bytes(cfg, 1, prompt_len + i) for i in range(steps)])
+    head_avg_ms = head_ms / max(head_n, 1)
+    head_b = lm_head_bytes(cfg, 1)
+    achieved = head_b / (head_avg_ms / 1e3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights (model.py distributions, Wo/proj dense), random prompt ids",
+        "config": {"workload": "cfg2: 155M (d768 L11 H6x128), batch 1, 32-token prompt, greedy decode "
+                               "to context 1024", "global_batch": 1, "seq_len": 1024,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv<1,32,EPI_LOGITS,rms> (lm_head + softcap)",
+                     "bytes_per_launch": head_b, "avg_launch_us": round(head_avg_ms * 1e3, 3),
+                     "launches": head_n},
+    }
+    step_gbs = avg_bytes / (ms / steps / 1e3) / 1e9
+    sec = {"b1_step": {"avg_alg_bytes": int(avg_bytes), "achieved_GBs": round(step_gbs, 1),
+                       "hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                       "wall_tok_s": round(toks / wall, 2)}}
+    del eng
+    torch.cuda.empty_cache()
+
+    if not args.no_secondary:
+        B, P, S = 64, 512, 512
+        eng = Engine(cfg, params, max_batch=B, max_ctx=1024, max_tokens=B * P)
+        pr = np.random.default_rng(2).integers(0, 50257, (B, P))
+        eng.prefill(pr, 0.8, 50, 7, 0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        e0.record()
+        for _ in range(reps):
+            eng.prefill(pr, 0.8, 50, 7, 0)
+        e1.record()
+        torch.cuda.synchronize()
+        pms = e0.elapsed_time(e1) / reps
+        pf = prefill_flops(cfg, B, P)
+        ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7, prof=False)
+        b64_bytes = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
+        b64_gbs = b64_bytes / (ms64 / S / 1e3) / 1e9
+        sec["b64_decode"] = {"tok_s": round(toks64 / (ms64 / 1e3), 1), "ms_per_step": round(ms64 / S, 4),
+                             "achieved_GBs": round(b64_gbs, 1), "hbm_frac": round(b64_gbs / HBM_PEAK_GBS, 4),
+                             "workload": "cfg3: B=64, 512-token prompts, 512 steps, T=0.8, top-k 50"}
+        tf = pf / (pms / 1e3) / 1e12
+        sec["b64_prefill"] = {"ms": round(pms, 3), "tok_s": round(B * P / (pms / 1e3), 1),
+                              "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_TFLOPS, 4),
+                              "flops": pf}
+        del eng
+        torch.cuda.empty_cache()
+    out["secondary"] = sec
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg, params, prompt_len, 1024)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

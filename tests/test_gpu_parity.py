@@ -1,0 +1,270 @@
+"""Parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars (the north star's): softcapped logits within 2e-2 max-abs of the oracle,
+greedy token sequences identical (64 steps on the 155M model); kernels
+against the reference's own known-answer tests at their tolerances.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.ref_model as R
+import oracle.ref_sample as S
+from attention_nn_amd.config import GPTConfig, cfg_155m, cfg_small_h4
+from attention_nn_amd.weights import init_params, perturb_lambdas
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import attention_nn_amd._lib as L
+    L.lib()   # the native library must load; no fallback exists
+
+
+def small_cfgs():
+    return {
+        "dh64": GPTConfig(vocab_size=512, num_layers=2, num_heads=2, model_dim=128, seq_len=64,
+                          window=16, long_layers=(1,)),
+        "dh128": GPTConfig(vocab_size=1000, num_layers=3, num_heads=2, model_dim=256, seq_len=96,
+                           window=8, long_layers=(0, 2)),
+    }
+
+
+def _engine(cfg, params, B, ctx=None, tokens=None):
+    from attention_nn_amd.engine import Engine
+    ctx = ctx or cfg.seq_len
+    return Engine(cfg, params, max_batch=B, max_ctx=ctx, max_tokens=tokens or B * ctx)
+
+
+# ---- operators: the reference self-tests on the HIP kernels ----------------
+
+def test_relu2_kernel_kat():
+    from attention_nn_amd import kernels as K
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((64, 33)).astype(np.float32)
+    y = K.relu2(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.allclose(y, np.maximum(x, 0) ** 2, atol=1e-6)          # metal_kernels.py:342
+    xb = torch.from_numpy(rng.standard_normal((128, 128)).astype(np.float32)).cuda().bfloat16()
+    yb = K.relu2(xb)
+    assert yb.dtype == torch.bfloat16                                  # metal_kernels.py:403
+    assert torch.equal(yb.float().cpu(), R.relu2(xb.float().cpu()))
+
+
+def test_rope_kernel_kat():
+    from attention_nn_amd import kernels as K
+    rng = np.random.default_rng(0)
+    B, T, H, D = 2, 16, 3, 64
+    cs, sn = K.make_rope_tables(T, D)
+    csr, snr = R.rope_tables(T, D)
+    assert torch.allclose(cs.cpu(), csr, atol=1e-6) and torch.allclose(sn.cpu(), snr, atol=1e-6)
+    x = rng.standard_normal((B, T, H, D)).astype(np.float32)
+    out = K.rope_ht(torch.from_numpy(x).cuda(), cs, sn).cpu().numpy()
+    from tests.test_oracle import _rope_reference_loop
+    ref = _rope_reference_loop(x, cs.cpu().numpy(), sn.cpu().numpy())
+    assert np.allclose(out, ref, atol=1e-5)                            # metal_kernels.py:363
+    back = K.rope_ht(torch.from_numpy(out).cuda(), cs, sn, inverse=True).cpu().numpy()
+    assert np.allclose(back, x, atol=1e-5)
+    # explicit position offset == rows of a longer sequence
+    cs2, sn2 = K.make_rope_tables(64, D)
+    a = K.rope_ht(torch.from_numpy(x).cuda(), cs2, sn2, pos0=20).cpu().numpy()
+    r = _rope_reference_loop(x, cs2.cpu().numpy()[20:36], sn2.cpu().numpy()[20:36])
+    assert np.allclose(a, r, atol=1e-5)
+    assert K.rope_ht(torch.from_numpy(x).cuda().bfloat16(), cs, sn).dtype == torch.bfloat16
+
+
+def test_rope_tables_long():
+    from attention_nn_amd import kernels as K
+    cs, sn = K.make_rope_tables(8192, 128)
+    csr, snr = R.rope_tables(8192, 128)
+    # theta up to 8191 rad: fp32 argument rounding dominates
+    assert (cs.cpu() - csr).abs().max().item() < 2e-3
+    assert (sn.cpu() - snr).abs().max().item() < 2e-3
+
+
+def test_rms_kernel():
+    from attention_nn_amd import kernels as K
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((7, 768)).astype(np.float32) * 3
+    y = K.rms(torch.from_numpy(x).cuda()).cpu()
+    assert torch.allclose(y, R.rms_f32(torch.from_numpy(x)), atol=1e-5)
+    xb = torch.from_numpy(x).cuda().bfloat16()
+    yb = K.rms(xb).float().cpu()
+    ref = R.rms(xb.float().cpu())
+    assert (yb - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
+
+
+# ---- whole forward -------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["dh64", "dh128"])
+@pytest.mark.parametrize("B,T", [(1, 5), (2, 40), (3, 1)])
+def test_forward_logits_parity(name, B, T):
+    cfg = small_cfgs()[name]
+    p = perturb_lambdas(init_params(cfg, 11, dense=True))
+    tok = np.random.default_rng(B * 100 + T).integers(0, cfg.vocab_size, (B, T))
+    print(f"case {name} B={B} T={T}", flush=True)
+    eng = _engine(cfg, p, B)
+    got = eng.forward_logits(tok).cpu()
+    ref = R.logits(cfg, p, tok)
+    err = (got - ref).abs().max().item()
+    assert err < LOGIT_TOL, err
+    assert torch.all((got > 0) & (got < 23))
+
+
+@pytest.mark.parametrize("name", ["dh64", "dh128"])
+def test_decode_teacher_forced_past_window(name):
+    """Decode logits at every position (well past the window) match the
+    oracle's KV-cache forward on the same tokens."""
+    cfg = small_cfgs()[name]
+    p = perturb_lambdas(init_params(cfg, 5, dense=True))
+    B, T0, steps = 2, 7, cfg.seq_len - 7
+    tok = np.random.default_rng(1).integers(0, cfg.vocab_size, (B, T0 + steps))
+    eng = _engine(cfg, p, B)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :T0], want_logits=True)
+    ref = R.forward(prep, tok[:, :T0], cache)[:, -1]
+    worst = (lg.cpu() - ref).abs().max().item()
+    for i in range(steps - 1):
+        t = tok[:, T0 + i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    assert worst < LOGIT_TOL, worst
+
+
+def test_batch_rows_independent():
+    cfg = small_cfgs()["dh128"]
+    p = perturb_lambdas(init_params(cfg, 2, dense=True))
+    tok = np.random.default_rng(3).integers(0, cfg.vocab_size, (3, 12))
+    eng3 = _engine(cfg, p, 3)
+    eng1 = _engine(cfg, p, 1)
+    a = eng3.forward_logits(tok).cpu()
+    for b in range(3):
+        c = eng1.forward_logits(tok[b:b + 1]).cpu()
+        assert (a[b] - c[0]).abs().max().item() < LOGIT_TOL
+
+
+def _greedy_oracle(cfg, params, prompt, steps):
+    prep = R.Prepared(cfg, params)
+    cache = R.KVCache(cfg.num_layers)
+    lg = R.forward(prep, prompt[None, :], cache)[0, -1]
+    out, logits = [], []
+    for _ in range(steps):
+        nxt = int(np.argmax(lg[:50257].numpy()))
+        out.append(nxt)
+        logits.append(lg)
+        lg = R.forward(prep, [[nxt]], cache)[0, -1]
+    return out, logits
+
+
+def _greedy_gpu(eng, prompt, steps):
+    nxt, lg = eng.prefill(prompt[None, :], want_logits=True)
+    out, logits = [int(nxt.item())], [lg[0].cpu()]
+    for _ in range(steps - 1):
+        nxt, lg = eng.decode(nxt, want_logits=True, out=nxt)
+        out.append(int(nxt.item()))
+        logits.append(lg[0].cpu())
+    return out, logits
+
+
+def test_greedy_155m_identical_64_steps():
+    """North-star gate: 155M (d768 L11 H6x128), dense random init, 32-token
+    prompt, 64 greedy steps identical to the oracle; per-step logits <= 2e-2."""
+    cfg = cfg_155m()
+    p = init_params(cfg, 0, dense=True)
+    prompt = np.random.default_rng(0).integers(0, 50257, 32)
+    eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+    got, glog = _greedy_gpu(eng, prompt, 64)
+    ref, rlog = _greedy_oracle(cfg, p, prompt, 64)
+    n_same = next((i for i, (a, b) in enumerate(zip(got, ref)) if a != b), 64)
+    worst = max((g - r).abs().max().item() for g, r in zip(glog[:n_same], rlog[:n_same]))
+    assert worst < LOGIT_TOL, worst
+    assert got == ref, f"first divergence at step {n_same}"
+
+
+def test_degenerate_init_repeats_last_token():
+    """cfg1 as specified (model.py init: Wo = proj = x0 = 0): greedy repeats
+    the last prompt token; logits equal the oracle's closed form."""
+    cfg = cfg_small_h4()
+    p = init_params(cfg, 0)
+    prompt = np.random.default_rng(1).integers(0, 50257, 16)
+    eng = _engine(cfg, p, 1, ctx=128, tokens=128)
+    got, glog = _greedy_gpu(eng, prompt, 16)
+    assert got == [int(prompt[-1])] * 16
+    ka = R.degenerate_known_answer(cfg, p, prompt[None, -1:])[0, -1]
+    assert (glog[0] - ka).abs().max().item() < LOGIT_TOL
+
+
+# ---- sampling ---------------------------------------------------------------
+
+def test_sampling_matches_oracle_draws():
+    cfg = small_cfgs()["dh128"]
+    p = init_params(cfg, 9, dense=True)
+    p["lm_head"] = p["lm_head"] * 60    # spread the logits so top-k matters
+    B = 4
+    tok = np.random.default_rng(6).integers(0, cfg.vocab_size, (B, 10))
+    eng = _engine(cfg, p, B)
+    for step, (temp, k) in enumerate([(0.8, 50), (1.0, 5), (0.5, 0), (2.0, 1), (0.8, 2000)]):
+        nxt, lg = eng.prefill(tok, temp, k, seed=1234, step=step, want_logits=True)
+        lg = lg.cpu().numpy()
+        for b in range(B):
+            z = lg[b, :min(50257, cfg.vocab_size)]
+            want = _sample_small(z, temp, k, S.uniform(1234, step, b))
+            assert int(nxt[b]) == want, (step, b)
+
+
+def _sample_small(z, temp, k, u):
+    zt = z.astype(np.float32) / np.float32(temp)
+    if k and k < zt.size:
+        kth = np.sort(zt)[-k]
+        keep = np.nonzero(zt >= kth)[0]
+    else:
+        keep = np.arange(zt.size)
+    w = np.exp(zt[keep].astype(np.float64) - zt[keep].max())
+    c = np.cumsum(w)
+    i = int(np.searchsorted(c, u * c[-1], side="right"))
+    return int(keep[min(i, keep.size - 1)])
+
+
+def test_sampling_chi_square():
+    cfg = small_cfgs()["dh64"]
+    p = init_params(cfg, 4, dense=True)
+    p["lm_head"] = p["lm_head"] * 300
+    tok = np.random.default_rng(2).integers(0, cfg.vocab_size, (1, 6))
+    eng = _engine(cfg, p, 1)
+    _, lg = eng.prefill(tok, want_logits=True)
+    z = lg[0].cpu().numpy()
+    temp, k, n = 1.0, 8, 3000
+    zt = z.astype(np.float32) / np.float32(temp)
+    kth = np.sort(zt)[-k]
+    keep = zt >= kth
+    w = np.where(keep, np.exp(zt.astype(np.float64) - zt.max()), 0.0)
+    prob = w / w.sum()
+    draws = [int(eng.prefill(tok, temp, k, seed=77, step=i)[0].item()) for i in range(n)]
+    counts = np.bincount(draws, minlength=z.size)
+    assert counts[~keep].sum() == 0
+    m = prob * n > 5
+    chi2 = (((counts - prob * n) ** 2)[m] / (prob * n)[m]).sum()
+    assert chi2 < 30.0, chi2      # <= 7 dof
+
+
+def test_sample_api_slides_window_like_reference():
+    """sample() past seq_len re-encodes ids[-seq_len:] from position 0
+    (sample.py:43), exactly like the reference's recompute loop."""
+    from attention_nn_amd.sample import sample
+    cfg = small_cfgs()["dh64"]
+    p = perturb_lambdas(init_params(cfg, 8, dense=True))
+    prompt = list(np.random.default_rng(4).integers(0, cfg.vocab_size, 50))
+    got = sample(prompt, 30, temperature=0.0, params=p, cfg=cfg)
+    ids = list(prompt)
+    for _ in range(30):
+        ctx = np.array(ids[-cfg.seq_len:])[None, :]
+        lg = R.logits(cfg, p, ctx)[0, -1]
+        ids.append(int(np.argmax(lg.numpy())))
+    assert got == ids[50:]
