@@ -136,6 +136,40 @@ def cpu_baseline(cfg, params, prompt_len, ctx_end, budget_s=20.0):
     }
 
 
+def secondary_b64(cfg, params):
+    """B=64, 512-token prompts: prefill vs MFMA, 512 decode steps vs HBM."""
+    import torch
+    from attention_nn_amd.engine import Engine
+    B, P, S = 64, 512, 512
+    eng = Engine(cfg, params, max_batch=B, max_ctx=1024, max_tokens=B * P)
+    pr = np.random.default_rng(2).integers(0, 50257, (B, P))
+    eng.prefill(pr, 0.8, 50, 7, 0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    e0.record()
+    for _ in range(reps):
+        eng.prefill(pr, 0.8, 50, 7, 0)
+    e1.record()
+    torch.cuda.synchronize()
+    pms = e0.elapsed_time(e1) / reps
+    pf = prefill_flops(cfg, B, P)
+    ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7, prof=False)
+    b64_bytes = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
+    b64_gbs = b64_bytes / (ms64 / S / 1e3) / 1e9
+    tf = pf / (pms / 1e3) / 1e12
+    del eng
+    torch.cuda.empty_cache()
+    return {
+        "b64_decode": {"tok_s": round(toks64 / (ms64 / 1e3), 1), "ms_per_step": round(ms64 / S, 4),
+                       "achieved_GBs": round(b64_gbs, 1), "hbm_frac": round(b64_gbs / HBM_PEAK_GBS, 4),
+                       "workload": "cfg3: B=64, 512-token prompts, 512 steps, T=0.8, top-k 50"},
+        "b64_prefill": {"ms": round(pms, 3), "tok_s": round(B * P / (pms / 1e3), 1),
+                        "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_TFLOPS, 4),
+                        "flops": pf},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +177,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-b64", action="store_true",
+                    help="run only the batch-64 prefill/decode section (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the decode path runs on a single MI355X "
@@ -161,6 +197,9 @@ def main():
     prompt_len = 32
     steps = min(args.steps, 1024 - prompt_len)
     prompt = np.random.default_rng(0).integers(0, 50257, (1, prompt_len))
+    if args.only_b64:
+        print(json.dumps(secondary_b64(cfg, params)), flush=True)
+        return 0
     eng = Engine(cfg, params, max_batch=1, max_ctx=1024, max_tokens=1024)
     ms, wall, (head_ms, head_n), toks = run_decode(eng, prompt, steps, args.warmup, 0.0, 0, 0)
     value = toks / (ms / 1e3)
@@ -198,32 +237,7 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.no_secondary:
-        B, P, S = 64, 512, 512
-        eng = Engine(cfg, params, max_batch=B, max_ctx=1024, max_tokens=B * P)
-        pr = np.random.default_rng(2).integers(0, 50257, (B, P))
-        eng.prefill(pr, 0.8, 50, 7, 0)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 3
-        e0.record()
-        for _ in range(reps):
-            eng.prefill(pr, 0.8, 50, 7, 0)
-        e1.record()
-        torch.cuda.synchronize()
-        pms = e0.elapsed_time(e1) / reps
-        pf = prefill_flops(cfg, B, P)
-        ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7, prof=False)
-        b64_bytes = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
-        b64_gbs = b64_bytes / (ms64 / S / 1e3) / 1e9
-        sec["b64_decode"] = {"tok_s": round(toks64 / (ms64 / 1e3), 1), "ms_per_step": round(ms64 / S, 4),
-                             "achieved_GBs": round(b64_gbs, 1), "hbm_frac": round(b64_gbs / HBM_PEAK_GBS, 4),
-                             "workload": "cfg3: B=64, 512-token prompts, 512 steps, T=0.8, top-k 50"}
-        tf = pf / (pms / 1e3) / 1e12
-        sec["b64_prefill"] = {"ms": round(pms, 3), "tok_s": round(B * P / (pms / 1e3), 1),
-                              "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_TFLOPS, 4),
-                              "flops": pf}
-        del eng
-        torch.cuda.empty_cache()
+        sec.update(secondary_b64(cfg, params))
     out["secondary"] = sec
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, params, prompt_len, 1024)
