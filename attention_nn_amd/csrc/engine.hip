@@ -15,6 +15,7 @@
 // `proj` is the GEMV (M <= 8) or the MFMA GEMM.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <string>
 #include <vector>
@@ -73,14 +74,21 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, x, x0, qkv, q, ao, hid, rs, part, zb, total;
+  size_t pos, sp, steps, amax, skcnt, skpart, x, x0, qkv, q, ao, hid, rs, part, zb, total;
 };
+constexpr int SK_MAX_TILES = 4096;          // split-K counters of the skinny GEMM
+constexpr size_t SK_PART_FLOATS = 512 * 1024;  // split-K partial tiles (<= 512 of 1024)
 
 SLayout ws_layout(const ann_config& c) {
   const size_t d = c.d, M = c.max_tokens, B = c.max_batch, Dh = d / c.H;
   SLayout s{};
   size_t off = 0;
   s.pos = off; off += up(B * 4);
+  s.sp = off; off += up(sizeof(SampParams));
+  s.steps = off; off += up(B * 8);
+  s.amax = off; off += up((B <= 8 ? B : 1) * (size_t)gemv_blocks(c.V, c.d) * 8);
+  s.skcnt = off; off += up(SK_MAX_TILES * 4);
+  s.skpart = off; off += up(SK_PART_FLOATS * 4);
   s.x = off; off += up(M * d * 2);
   s.x0 = off; off += up(M * d * 2);
   s.qkv = off; off += up(M * 3 * d * 2);
@@ -119,6 +127,8 @@ int check_config(const ann_config* c) {
   if (c->max_tokens < c->max_batch)
     return fail(ANN_E_ARG, "max_tokens=%d < max_batch=%d", c->max_tokens, c->max_batch);
   if (!(c->rms_eps > 0.f)) return fail(ANN_E_ARG, "rms_eps must be positive");
+  if (!(c->attn_scale > 0.f) || c->attn_scale * Dh > 40.f)
+    return fail(ANN_E_ARG, "attn_scale * head_dim must lie in (0, 40] (bounded-score softmax)");
   return ANN_OK;
 }
 
@@ -135,6 +145,23 @@ struct ann_ctx {
   bool bound = false;
   int len = 0;  // tokens held per sequence
   int B = 0;    // sequences held
+  // decode-step graph (captured once per key, replayed every step)
+  bool use_graph = true;
+  hipStream_t cap_st = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  struct GKey {
+    int B;
+    const int32_t* tok;
+    int32_t* out;
+    float* logits;
+    bool greedy;
+  } gkey{};
+  // host mirror of the device sampling parameters
+  bool sp_valid = false;
+  float sp_temp = 0.f;
+  int sp_topk = 0;
+  uint64_t sp_seed = 0, sp_step = 0;
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -172,21 +199,34 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
   }
 };
 
-// y = (rms?)(X) @ W^T for M rows with the given epilogue.
-int proj(ann_ctx* c, int kind, int epi, bool rms, const bf16_t* W, const bf16_t* X, int ldx,
-         int M, int N, int K, EpiArgs ea, hipStream_t st) {
+// y = pre(X) @ W^T for M rows with the given epilogue.
+int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
+         int M, int N, int K, EpiArgs ea, hipStream_t st, PreArgs pa = PreArgs{}) {
   float* rs = nullptr;
   const bool use_gemv = gemv_fits(M, K);
-  if (rms && !use_gemv) {
+  if (pre == PRE_ATTN && !use_gemv) return fail(ANN_E_ARG, "attention prologue needs the GEMV");
+  if (pre == PRE_RMS && !use_gemv && M > 64) {
     rs = c->sp<float>(c->sl.rs);
     HIPCHK(row_rms_scale(X, ldx, rs, M, K, c->c.rms_eps, st));
   }
   ProfScope ps(c, kind, st);
   if (use_gemv)
-    HIPCHK(gemv(epi, rms, W, X, ldx, M, N, K, c->c.rms_eps, ea, st));
+    HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, pa, st));
+  else if (M <= 64 && (pre == PRE_RMS || (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <=
+                                              SK_PART_FLOATS))
+    HIPCHK(gemm_skinny(epi, pre == PRE_RMS, X, ldx, W, M, N, K, c->c.rms_eps, ea,
+                       c->sp<float>(c->sl.skpart), c->sp<unsigned>(c->sl.skcnt), st));
   else
     HIPCHK(gemm(epi, X, ldx, rs, W, M, N, K, ea, st));
   return ANN_OK;
+}
+
+// Fixed split counts of the decode attention (independent of the current
+// length, so a captured step replays for every position).
+int dec_splits(const ann_config& g, bool lng) {
+  const int keys = lng ? g.max_ctx : (g.window < g.max_ctx ? g.window : g.max_ctx);
+  int n = (keys + 63) / 64;
+  return n < 1 ? 1 : (n > MAX_SPLIT ? MAX_SPLIT : n);
 }
 
 // embed + all layers for M = B*T rows whose positions start at pos[b].
@@ -211,37 +251,51 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
     EpiArgs ea{};
     ea.out = qkv;
     ea.ldo = 3 * d;
-    int rc = proj(c, ANN_PROF_QKV, EPI_STORE, true, c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d, ea, st);
+    int rc = proj(c, ANN_PROF_QKV, EPI_STORE, PRE_RMS, c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d,
+                  ea, st);
     if (rc) return rc;
-    HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,
-                    g.rms_eps, st));
-    int nsplit = 1;
-    if (T == 1) {  // decode: split long key ranges so B*H*nsplit fills the GPU
-      const int n = lng ? c->len + 1 : (c->len + 1 < g.window ? c->len + 1 : g.window);
-      const int chunks = (n + 63) / 64;
-      int want = (512 + B * H - 1) / (B * H);
-      nsplit = chunks < want ? chunks : want;
-      if (nsplit > MAX_SPLIT) nsplit = MAX_SPLIT;
-      if (nsplit < 1) nsplit = 1;
-    }
-    {
-      ProfScope ps(c, ANN_PROF_ATTN, st);
-      HIPCHK(attention(q, c->kcache(l), c->vcache(l), pos, ao, part, M, T, H, Dh, g.max_ctx,
-                       g.window, lng, g.attn_scale, nsplit, st));
-    }
     EpiArgs er{};
     er.x = x;
     er.x0 = x0;
     er.ldr = d;
     er.lam = lam + 8 * l;
-    rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, false, c->layer_w(l, c->wl.o), ao, d, M, d, d, er, st);
-    if (rc) return rc;
+    if (T == 1) {  // decode: fused QK-norm / RoPE / KV append, split partials
+      const int ns = dec_splits(g, lng);
+      {
+        ProfScope ps(c, ANN_PROF_ATTN, st);
+        HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part, B, H, Dh,
+                           g.max_ctx, g.window, lng, g.attn_scale, g.rms_eps, ns, st));
+      }
+      if (gemv_fits(M, d) && H <= 16) {
+        PreArgs pa{part, H, Dh, ns};
+        rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_ATTN, c->layer_w(l, c->wl.o), nullptr, d, M,
+                  d, d, er, st, pa);
+      } else {
+        HIPCHK(attn_decode_combine(part, ao, B, H, Dh, ns, st));
+        rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d,
+                  d, er, st);
+      }
+      if (rc) return rc;
+    } else {
+      HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,
+                      g.rms_eps, st));
+      {
+        ProfScope ps(c, ANN_PROF_ATTN, st);
+        HIPCHK(attention(q, c->kcache(l), c->vcache(l), pos, ao, part, M, T, H, Dh, g.max_ctx,
+                         g.window, lng, g.attn_scale, 1, st));
+      }
+      rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d, d,
+                er, st);
+      if (rc) return rc;
+    }
     EpiArgs eh{};
     eh.out = hid;
     eh.ldo = 4 * d;
-    rc = proj(c, ANN_PROF_FC, EPI_RELU2, true, c->layer_w(l, c->wl.fc), x, d, M, 4 * d, d, eh, st);
+    rc = proj(c, ANN_PROF_FC, EPI_RELU2, PRE_RMS, c->layer_w(l, c->wl.fc), x, d, M, 4 * d, d, eh,
+              st);
     if (rc) return rc;
-    rc = proj(c, ANN_PROF_PROJ, EPI_RESID_MLP, false, c->layer_w(l, c->wl.proj), hid, 4 * d, M, d, 4 * d, er, st);
+    rc = proj(c, ANN_PROF_PROJ, EPI_RESID_MLP, PRE_PLAIN, c->layer_w(l, c->wl.proj), hid, 4 * d, M,
+              d, 4 * d, er, st);
     if (rc) return rc;
   }
   return ANN_OK;
@@ -261,20 +315,91 @@ int check_sampling(const ann_ctx* c, const ann_sampling* s) {
   return ANN_OK;
 }
 
-// z of the last row of each sequence -> sampled token.
-int head_and_sample(ann_ctx* c, int B, int T, const ann_sampling* s, int32_t* out_tok,
-                    float* logits, hipStream_t st) {
+// z of the last row of each sequence -> sampled token; positions advance by
+// pos_adv (the tokens this call added).  Sampling parameters come from the
+// device copy written by sync_sampling.
+int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, float* logits,
+                    int pos_adv, hipStream_t st) {
   const ann_config& g = c->c;
   bf16_t* x = c->sp<bf16_t>(c->sl.x);
   bf16_t* zb = c->sp<bf16_t>(c->sl.zb);
+  int32_t* pos = c->sp<int32_t>(c->sl.pos);
   EpiArgs ez{};
-  ez.z = zb;
   ez.logits = logits;
   ez.ldz = g.V;
-  int rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, true, c->wptr(c->wl.head), x + (size_t)(T - 1) * g.d, T * g.d, B,
-                g.V, g.d, ez, st);
+  const bool fused_greedy = greedy && gemv_fits(B, g.d);
+  unsigned long long* keys = c->sp<unsigned long long>(c->sl.amax);
+  if (fused_greedy) {
+    ez.amax = keys;
+    ez.Vs = g.V_sample;
+  } else {
+    ez.z = zb;
+  }
+  int rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, PRE_RMS, c->wptr(c->wl.head),
+                x + (size_t)(T - 1) * g.d, T * g.d, B, g.V, g.d, ez, st);
   if (rc) return rc;
-  HIPCHK(sample(zb, g.V, B, g.V_sample, s->temperature, s->top_k, s->seed, s->step, out_tok, st));
+  if (fused_greedy)
+    HIPCHK(argmax_finalize(keys, gemv_blocks(g.V, g.d), B, out_tok, pos, pos_adv, st));
+  else
+    HIPCHK(sample(zb, g.V, B, g.V_sample, c->sp<SampParams>(c->sl.sp),
+                  c->sp<unsigned long long>(c->sl.steps), out_tok, pos, pos_adv, st));
+  return ANN_OK;
+}
+
+// Bring the device sampling parameters / draw counters in line with s.
+int sync_sampling(ann_ctx* c, const ann_sampling* s, int B, hipStream_t st) {
+  const bool greedy = s->temperature == 0.f;
+  if (greedy) return ANN_OK;  // the greedy path reads no parameters
+  if (c->sp_valid && c->sp_temp == s->temperature && c->sp_topk == s->top_k &&
+      c->sp_seed == s->seed && c->sp_step == s->step)
+    return ANN_OK;
+  HIPCHK(set_sampling(c->sp<SampParams>(c->sl.sp), c->sp<unsigned long long>(c->sl.steps), B,
+                      s->temperature, s->top_k, s->seed, s->step, st));
+  c->sp_valid = true;
+  c->sp_temp = s->temperature;
+  c->sp_topk = s->top_k;
+  c->sp_seed = s->seed;
+  c->sp_step = s->step;
+  return ANN_OK;
+}
+
+void drop_graph(ann_ctx* c) {
+  if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+  if (c->graph) (void)hipGraphDestroy(c->graph);
+  c->gexec = nullptr;
+  c->graph = nullptr;
+}
+
+int enqueue_decode(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
+                   float* logits, hipStream_t st) {
+  int rc = run_body(c, tokens, B, 1, st);
+  if (rc) return rc;
+  return head_and_sample(c, B, 1, greedy, out_tok, logits, 1, st);
+}
+
+// Capture one decode step into a graph (once per key) and launch it.
+int decode_graph(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
+                 float* logits, hipStream_t st) {
+  const ann_ctx::GKey key{B, tokens, out_tok, logits, greedy};
+  const bool same = c->gexec && key.B == c->gkey.B && key.tok == c->gkey.tok &&
+                    key.out == c->gkey.out && key.logits == c->gkey.logits &&
+                    key.greedy == c->gkey.greedy;
+  if (!same) {
+    drop_graph(c);
+    if (!c->cap_st) HIPCHK(hipStreamCreateWithFlags(&c->cap_st, hipStreamNonBlocking));
+    HIPCHK(hipStreamBeginCapture(c->cap_st, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_decode(c, tokens, B, greedy, out_tok, logits, c->cap_st);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->cap_st, &g);
+    if (rc || e != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc ? rc : fail(ANN_E_HIP, "graph capture failed: %s", hipGetErrorString(e));
+    }
+    c->graph = g;
+    HIPCHK(hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0));
+    c->gkey = key;
+  }
+  HIPCHK(hipGraphLaunch(c->gexec, st));
   return ANN_OK;
 }
 
@@ -295,6 +420,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->Dh = cfg->d / cfg->H;
   c->wl = weight_layout(*cfg);
   c->sl = ws_layout(*cfg);
+  const char* ge = getenv("ANN_DECODE_GRAPH");
+  c->use_graph = !(ge && ge[0] == '0');
   *out = c;
   return ANN_OK;
 }
@@ -302,6 +429,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
 void ann_destroy(ann_ctx* ctx) {
   if (!ctx) return;
   for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
+  drop_graph(ctx);
+  if (ctx->cap_st) (void)hipStreamDestroy(ctx->cap_st);
   delete ctx;
 }
 
@@ -393,6 +522,8 @@ int ann_bind(ann_ctx* c, void* wbuf, size_t wbytes, void* kv, size_t kvbytes, vo
     return fail(ANN_E_CAPACITY, "workspace %zu bytes < required %zu", wsbytes, c->sl.total);
   if (((uintptr_t)wbuf | (uintptr_t)kv | (uintptr_t)workspace) & 255)
     return fail(ANN_E_ARG, "buffers must be 256-byte aligned");
+  drop_graph(c);
+  c->sp_valid = false;
   c->w = (uint8_t*)wbuf;
   c->kv = (uint8_t*)kv;
   c->ws = (uint8_t*)workspace;
@@ -438,8 +569,8 @@ int ann_forward_logits(ann_ctx* c, const int32_t* tokens, int32_t B, int32_t T, 
   EpiArgs ez{};
   ez.logits = logits;
   ez.ldz = c->c.V;
-  rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, true, c->wptr(c->wl.head), c->sp<bf16_t>(c->sl.x), c->c.d, B * T,
-            c->c.V, c->c.d, ez, st);
+  rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, PRE_RMS, c->wptr(c->wl.head), c->sp<bf16_t>(c->sl.x),
+            c->c.d, B * T, c->c.V, c->c.d, ez, st);
   if (rc) return rc;
   HIPCHK(advance_pos(pos, B, T, st));
   c->len = T;
@@ -458,11 +589,13 @@ int ann_prefill(ann_ctx* c, const int32_t* tokens, int32_t B, int32_t T, const a
   HIPCHK(set_pos(pos, B, 0, st));
   c->len = 0;
   c->B = B;
+  rc = sync_sampling(c, s, B, st);
+  if (rc) return rc;
   rc = run_body(c, tokens, B, T, st);
   if (rc) return rc;
-  rc = head_and_sample(c, B, T, s, out_tok, logits, st);
+  rc = head_and_sample(c, B, T, s->temperature == 0.f, out_tok, logits, T, st);
   if (rc) return rc;
-  HIPCHK(advance_pos(pos, B, T, st));
+  if (s->temperature != 0.f) c->sp_step += 1;
   c->len = T;
   return ANN_OK;
 }
@@ -479,11 +612,15 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   if (c->len + 1 > c->c.max_ctx)
     return fail(ANN_E_CAPACITY, "context %d would exceed max_ctx=%d", c->len + 1, c->c.max_ctx);
   hipStream_t st = (hipStream_t)stream;
-  rc = run_body(c, tokens, B, 1, st);
+  rc = sync_sampling(c, s, B, st);
   if (rc) return rc;
-  rc = head_and_sample(c, B, 1, s, out_tok, logits, st);
+  const bool greedy = s->temperature == 0.f;
+  if (c->use_graph && c->prof_kind < 0)
+    rc = decode_graph(c, tokens, B, greedy, out_tok, logits, st);
+  else
+    rc = enqueue_decode(c, tokens, B, greedy, out_tok, logits, st);
   if (rc) return rc;
-  HIPCHK(advance_pos(c->sp<int32_t>(c->sl.pos), B, 1, st));
+  if (!greedy) c->sp_step += 1;
   c->len += 1;
   return ANN_OK;
 }

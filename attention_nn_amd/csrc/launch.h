@@ -25,6 +25,28 @@ struct EpiArgs {
   bf16_t* z;         // LOGITS: bf16 z (M, ldz) or null
   float* logits;     // LOGITS: fp32 softcapped (M, ldz) or null
   int ldz;
+  // LOGITS + greedy (GEMV only): each work-group stores its best packed key
+  // (ordered z << 32 | ~n, over columns n < Vs) per row to
+  // amax[m * blocks + block]; argmax_finalize turns them into tokens.
+  unsigned long long* amax;
+  int Vs;
+};
+
+// Sampling parameters read by the sampler from device memory (so a captured
+// decode step replays with new values); step[b] counts draws per sequence.
+struct SampParams {
+  float temperature;
+  int top_k;
+  unsigned long long seed;
+};
+
+// Input prologue of the GEMV: X rows as given, RMS-normalised, or the
+// attention output rebuilt from decode-attention split partials.
+enum { PRE_PLAIN = 0, PRE_RMS = 1, PRE_ATTN = 2 };
+
+struct PreArgs {
+  const float* part;  // (M, H, nsplit, Dh + 1): O (Dh) then L
+  int H, Dh, nsplit;
 };
 
 hipError_t pack_transpose(const float* src, bf16_t* dst, int K, int N, int ldd,
@@ -42,10 +64,20 @@ hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const 
                     const float* cs, const float* sn, int M, int T, int H, int Dh, int max_ctx,
                     float eps, hipStream_t st);
 
-// GEMV for M <= 8 rows: y = (rms?)(X) @ W^T, X (M, ldx) bf16.
-hipError_t gemv(int epi, bool rms_in, const bf16_t* W, const bf16_t* X, int ldx, int M, int N,
-                int K, float eps, const EpiArgs& ea, hipStream_t st);
+// GEMV for M <= 8 rows: y = pre(X) @ W^T, X (M, ldx) bf16.
+hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int M, int N, int K,
+                float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st);
 bool gemv_fits(int M, int K);
+int gemv_blocks(int N, int K);
+hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
+                           int32_t* pos, int pos_adv, hipStream_t st);
+// Skinny MFMA GEMM for decode (M small, N moderate): y = (rms?)(A) @ W^T;
+// part / cnt: split-K scratch (tiles * ksplit * 1024 floats, tiles counters,
+// counters zero between calls).
+hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
+                       int K, float eps, const EpiArgs& ea, float* part, unsigned* cnt,
+                       hipStream_t st);
+int gemm_sk_split(int M, int N, int K);
 // MFMA GEMM: y = (rs_m * A) @ W^T with A (M, lda) bf16; rs null = no scaling.
 hipError_t gemm(int epi, const bf16_t* A, int lda, const float* rs, const bf16_t* W, int M,
                 int N, int K, const EpiArgs& ea, hipStream_t st);
@@ -57,9 +89,24 @@ hipError_t attention(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const 
                      bf16_t* out, float* part, int M, int T, int H, int Dh, int max_ctx,
                      int window, bool long_layer, float scale, int nsplit, hipStream_t st);
 
-// Sampling of B rows of bf16 z (B, ldz) over the first Vs entries.
-hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, float temperature, int top_k,
-                  uint64_t seed, uint64_t step, int32_t* out_tok, hipStream_t st);
+// Decode attention with fused QK-norm / RoPE / KV append (one token per
+// sequence); writes split partials (B, H, nsplit, Dh + 1).
+hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
+                       const float* cs, const float* sn, float* part, int B, int H, int Dh,
+                       int max_ctx, int window, bool long_layer, float scale, float eps,
+                       int nsplit, hipStream_t st);
+hipError_t attn_decode_combine(const float* part, bf16_t* out, int B, int H, int Dh, int nsplit,
+                               hipStream_t st);
+
+// Sampling of B rows of bf16 z (B, ldz) over the first Vs entries with the
+// device-resident parameters; uses and increments steps[b]; advances pos[b]
+// by pos_adv.
+hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
+                  unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
+                  hipStream_t st);
+hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
+                        int top_k, unsigned long long seed, unsigned long long step,
+                        hipStream_t st);
 hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st);
 hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st);
 

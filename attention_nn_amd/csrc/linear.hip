@@ -44,40 +44,67 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
 // ---- GEMV -------------------------------------------------------------------
 
 constexpr int GEMV_THREADS = 256;
-constexpr int GEMV_U = 4;  // 16-byte weight chunks in flight per lane
 
-template <int M, int LPR, int EPI, bool RMS>
-__global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict__ W,
-                                                       const bf16_t* __restrict__ X, int ldx,
-                                                       int N, int K, float eps, EpiArgs ea) {
-  extern __shared__ uint4 xs4[];                 // M * K bf16, normalised if RMS
-  __shared__ float red[M][GEMV_THREADS / 64];
+__device__ __forceinline__ uint32_t zkey(bf16_t h) {  // order-preserving 16-bit key
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
+}
+
+// Fill the LDS activation tile xs (M x K bf16) per the prologue PRE.
+template <int M, int PRE>
+__device__ __forceinline__ void gemv_prologue(uint4* xs4, const bf16_t* __restrict__ X, int ldx,
+                                              int K, float eps, const PreArgs& pa, float* red) {
   const int tid = threadIdx.x;
   const int K8 = K >> 3;
-
+  if (PRE == PRE_ATTN) {
+    // o[m][h*Dh + e] = sum_s O_s / sum_s L_s, rounded to bf16
+    const int Dh = pa.Dh, ns = pa.nsplit, st = Dh + 1, H = pa.H;
+    float* linv = red;   // M * H reciprocals of sum_s L_s (M * H <= 8 * 16)
+    for (int i = tid; i < M * H; i += GEMV_THREADS) {
+      const float* pp = pa.part + (size_t)i * ns * st + Dh;
+      float l = 0.f;
+      for (int s = 0; s < ns; ++s) l += pp[s * st];
+      linv[i] = 1.f / l;
+    }
+    __syncthreads();
+    bf16_t* xs = (bf16_t*)xs4;
+    for (int i = tid; i < M * K; i += GEMV_THREADS) {
+      const int m = i / K, k = i % K, h = k / Dh, e = k % Dh;
+      const float* pp = pa.part + ((size_t)m * H + h) * ns * st + e;
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+      int s = 0;
+      for (; s + 4 <= ns; s += 4) {
+        o0 += pp[s * st];
+        o1 += pp[(s + 1) * st];
+        o2 += pp[(s + 2) * st];
+        o3 += pp[(s + 3) * st];
+      }
+      for (; s < ns; ++s) o0 += pp[s * st];
+      xs[i] = f2bf(((o0 + o1) + (o2 + o3)) * linv[m * H + h]);
+    }
+    return;
+  }
   float scale[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) scale[m] = 1.f;
-  if (RMS) {
-    float ss[M];
+  if (PRE == PRE_RMS) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      ss[m] = 0.f;
+      float ss = 0.f;
       for (int c = tid; c < K8; c += GEMV_THREADS) {
         float f[8];
         unpack8(*(const uint4*)(X + (size_t)m * ldx + c * 8), f);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss[m] += f[j] * f[j];
+        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
       }
-      ss[m] = group_sum<64>(ss[m]);
-      if ((tid & 63) == 0) red[m][tid >> 6] = ss[m];
+      ss = group_sum<64>(ss);
+      if ((tid & 63) == 0) red[m * (GEMV_THREADS / 64) + (tid >> 6)] = ss;
     }
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < GEMV_THREADS / 64; ++w) t += red[m][w];
+      for (int w = 0; w < GEMV_THREADS / 64; ++w) t += red[m * (GEMV_THREADS / 64) + w];
       scale[m] = rsqrtf(t / (float)K + eps);
     }
   }
@@ -85,7 +112,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict_
   for (int m = 0; m < M; ++m) {
     for (int c = tid; c < K8; c += GEMV_THREADS) {
       uint4 v = *(const uint4*)(X + (size_t)m * ldx + c * 8);
-      if (RMS) {
+      if (PRE == PRE_RMS) {
         float f[8];
         unpack8(v, f);
         v.x = pack2(f[0] * scale[m], f[1] * scale[m]);
@@ -96,9 +123,20 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict_
       xs4[m * K8 + c] = v;
     }
   }
-  __syncthreads();
+}
 
-  constexpr int G = GEMV_THREADS / LPR;
+template <int M, int LPR, int EPI, int PRE, int GEMV_U>
+__global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict__ W,
+                                                       const bf16_t* __restrict__ X, int ldx,
+                                                       int N, int K, float eps, EpiArgs ea,
+                                                       PreArgs pa) {
+  extern __shared__ uint4 xs4[];                 // M * K bf16 activations
+  constexpr int G = GEMV_THREADS / LPR;          // weight rows per work-group
+  __shared__ float red[M * 16 > 128 ? M * 16 : 128];
+  __shared__ unsigned long long s_key[G][M];
+  const int tid = threadIdx.x;
+  const int K8 = K >> 3;
+
   const int g = tid / LPR, lig = tid % LPR;
   const int n = blockIdx.x * G + g;
   const bool live = n < N;
@@ -107,12 +145,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict_
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.f;
 
-  for (int c0 = 0; c0 < K8; c0 += LPR * GEMV_U) {
-    uint4 w[GEMV_U];
+  // the first GEMV_U weight chunks of this lane do not depend on the
+  // activations: issue them before the prologue so both latencies overlap
+  uint4 w[GEMV_U];
 #pragma unroll
-    for (int u = 0; u < GEMV_U; ++u) {
-      const int c = c0 + u * LPR + lig;
-      w[u] = (live && c < K8) ? wrow[c] : make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < GEMV_U; ++u) {
+    const int c = u * LPR + lig;
+    w[u] = (live && c < K8) ? wrow[c] : make_uint4(0, 0, 0, 0);
+  }
+  gemv_prologue<M, PRE>(xs4, X, ldx, K, eps, pa, red);
+  __syncthreads();
+
+  for (int c0 = 0; c0 < K8; c0 += LPR * GEMV_U) {
+    if (c0) {
+#pragma unroll
+      for (int u = 0; u < GEMV_U; ++u) {
+        const int c = c0 + u * LPR + lig;
+        w[u] = (live && c < K8) ? wrow[c] : make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int u = 0; u < GEMV_U; ++u) {
@@ -137,63 +187,136 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict_
     for (int m = 0; m < M; ++m)
       if (lig == m) epilogue<EPI>(ea, m, n, acc[m]);
   }
+  if (EPI == EPI_LOGITS && ea.amax) {
+    // greedy: per-row max of (z, lowest index) over this work-group's rows,
+    // stored to amax[m * gridDim.x + block]; k_argmax_finalize reduces them.
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (lig == m)
+        s_key[g][m] = (live && n < ea.Vs)
+            ? (((unsigned long long)zkey(f2bf(acc[m])) << 32) | (unsigned long long)(0xffffffffu - (unsigned)n))
+            : 0ull;
+    __syncthreads();
+    if (tid < M) {
+      unsigned long long best = 0;
+#pragma unroll
+      for (int i = 0; i < G; ++i) best = s_key[i][tid] > best ? s_key[i][tid] : best;
+      ea.amax[(size_t)tid * gridDim.x + blockIdx.x] = best;
+    }
+  }
+}
+
+// out_tok[m] = index of the largest key of row m (lowest index on ties),
+// pos[m] += pos_adv.  One work-group per row.
+__global__ __launch_bounds__(1024) void k_argmax_finalize(const unsigned long long* __restrict__ keys,
+                                                          int nkeys, int32_t* __restrict__ out_tok,
+                                                          int32_t* __restrict__ pos, int pos_adv) {
+  __shared__ unsigned long long red[16];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const unsigned long long* k = keys + (size_t)m * nkeys;
+  unsigned long long b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+  int i = tid;
+  for (; i + 3 * 1024 < nkeys; i += 4 * 1024) {
+    const unsigned long long v0 = k[i], v1 = k[i + 1024], v2 = k[i + 2048], v3 = k[i + 3072];
+    b0 = v0 > b0 ? v0 : b0;
+    b1 = v1 > b1 ? v1 : b1;
+    b2 = v2 > b2 ? v2 : b2;
+    b3 = v3 > b3 ? v3 : b3;
+  }
+  for (; i < nkeys; i += 1024) b0 = k[i] > b0 ? k[i] : b0;
+  b0 = b1 > b0 ? b1 : b0;
+  b2 = b3 > b2 ? b3 : b2;
+  unsigned long long best = b2 > b0 ? b2 : b0;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned lo = __shfl_xor((unsigned)best, o, 64);
+    const unsigned hi = __shfl_xor((unsigned)(best >> 32), o, 64);
+    const unsigned long long w = ((unsigned long long)hi << 32) | lo;
+    best = w > best ? w : best;
+  }
+  if ((tid & 63) == 0) red[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long b = red[0];
+    for (int w = 1; w < 16; ++w) b = red[w] > b ? red[w] : b;
+    out_tok[m] = (int32_t)(0xffffffffu - (unsigned)(b & 0xffffffffull));
+    if (pos) pos[m] += pos_adv;
+  }
+}
+
+int gemv_blocks(int N, int K) {
+  const int G = GEMV_THREADS / (K <= 1024 ? 32 : 64);
+  return (N + G - 1) / G;
+}
+
+hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
+                           int32_t* pos, int pos_adv, hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(1024), 0, st, keys, nkeys, out_tok, pos,
+                     pos_adv);
+  return hipGetLastError();
 }
 
 bool gemv_fits(int M, int K) {
   return M >= 1 && M <= 8 && (size_t)M * K * 2 <= 64 * 1024 && K % 8 == 0;
 }
 
-template <int M, int LPR, int EPI, bool RMS>
+// U = 16-byte weight chunks each lane keeps in flight: enough to hold the
+// whole row slice when K / (8 LPR) <= 8, without spilling for short rows.
+template <int M, int LPR, int EPI, int PRE>
 static hipError_t launch_gemv(const bf16_t* W, const bf16_t* X, int ldx, int N, int K, float eps,
-                              const EpiArgs& ea, hipStream_t st) {
+                              const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
   constexpr int G = GEMV_THREADS / LPR;
   dim3 grid((N + G - 1) / G);
   size_t lds = (size_t)M * K * 2;
-  hipLaunchKernelGGL((k_gemv<M, LPR, EPI, RMS>), grid, dim3(GEMV_THREADS), lds, st, W, X, ldx, N,
-                     K, eps, ea);
+  if ((K >> 3) <= 4 * LPR)
+    hipLaunchKernelGGL((k_gemv<M, LPR, EPI, PRE, 4>), grid, dim3(GEMV_THREADS), lds, st, W, X,
+                       ldx, N, K, eps, ea, pa);
+  else
+    hipLaunchKernelGGL((k_gemv<M, LPR, EPI, PRE, 8>), grid, dim3(GEMV_THREADS), lds, st, W, X,
+                       ldx, N, K, eps, ea, pa);
   return hipGetLastError();
 }
 
-template <int M, int EPI, bool RMS>
+template <int M, int EPI, int PRE>
 static hipError_t gemv_lpr(const bf16_t* W, const bf16_t* X, int ldx, int N, int K, float eps,
-                           const EpiArgs& ea, hipStream_t st) {
-  if (K <= 1024) return launch_gemv<M, 32, EPI, RMS>(W, X, ldx, N, K, eps, ea, st);
-  return launch_gemv<M, 64, EPI, RMS>(W, X, ldx, N, K, eps, ea, st);
+                           const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
+  if (K <= 1024) return launch_gemv<M, 32, EPI, PRE>(W, X, ldx, N, K, eps, ea, pa, st);
+  return launch_gemv<M, 64, EPI, PRE>(W, X, ldx, N, K, eps, ea, pa, st);
 }
 
 template <int M>
-static hipError_t gemv_m(int epi, bool rms, const bf16_t* W, const bf16_t* X, int ldx, int N,
-                         int K, float eps, const EpiArgs& ea, hipStream_t st) {
+static hipError_t gemv_m(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int N,
+                         int K, float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
+#define ANN_GEMV_PRE(E)                                                                 \
+  switch (pre) {                                                                        \
+    case PRE_PLAIN: return gemv_lpr<M, E, PRE_PLAIN>(W, X, ldx, N, K, eps, ea, pa, st); \
+    case PRE_RMS: return gemv_lpr<M, E, PRE_RMS>(W, X, ldx, N, K, eps, ea, pa, st);     \
+    case PRE_ATTN: return gemv_lpr<M, E, PRE_ATTN>(W, X, ldx, N, K, eps, ea, pa, st);   \
+  }                                                                                     \
+  break;
   switch (epi) {
-    case EPI_STORE:
-      return rms ? gemv_lpr<M, EPI_STORE, true>(W, X, ldx, N, K, eps, ea, st)
-                 : gemv_lpr<M, EPI_STORE, false>(W, X, ldx, N, K, eps, ea, st);
-    case EPI_RELU2:
-      return rms ? gemv_lpr<M, EPI_RELU2, true>(W, X, ldx, N, K, eps, ea, st)
-                 : gemv_lpr<M, EPI_RELU2, false>(W, X, ldx, N, K, eps, ea, st);
-    case EPI_RESID_ATTN:
-      return gemv_lpr<M, EPI_RESID_ATTN, false>(W, X, ldx, N, K, eps, ea, st);
-    case EPI_RESID_MLP:
-      return gemv_lpr<M, EPI_RESID_MLP, false>(W, X, ldx, N, K, eps, ea, st);
-    case EPI_LOGITS:
-      return rms ? gemv_lpr<M, EPI_LOGITS, true>(W, X, ldx, N, K, eps, ea, st)
-                 : gemv_lpr<M, EPI_LOGITS, false>(W, X, ldx, N, K, eps, ea, st);
+    case EPI_STORE: ANN_GEMV_PRE(EPI_STORE)
+    case EPI_RELU2: ANN_GEMV_PRE(EPI_RELU2)
+    case EPI_RESID_ATTN: ANN_GEMV_PRE(EPI_RESID_ATTN)
+    case EPI_RESID_MLP: ANN_GEMV_PRE(EPI_RESID_MLP)
+    case EPI_LOGITS: ANN_GEMV_PRE(EPI_LOGITS)
   }
+#undef ANN_GEMV_PRE
   return hipErrorInvalidValue;
 }
 
-hipError_t gemv(int epi, bool rms_in, const bf16_t* W, const bf16_t* X, int ldx, int M, int N,
-                int K, float eps, const EpiArgs& ea, hipStream_t st) {
+hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int M, int N, int K,
+                float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
   if (!gemv_fits(M, K)) return hipErrorInvalidValue;
   switch (M) {
-    case 1: return gemv_m<1>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 2: return gemv_m<2>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 3: return gemv_m<3>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 4: return gemv_m<4>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 5: return gemv_m<5>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 6: return gemv_m<6>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 7: return gemv_m<7>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
-    case 8: return gemv_m<8>(epi, rms_in, W, X, ldx, N, K, eps, ea, st);
+    case 1: return gemv_m<1>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 2: return gemv_m<2>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 3: return gemv_m<3>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 4: return gemv_m<4>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 5: return gemv_m<5>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 6: return gemv_m<6>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 7: return gemv_m<7>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 8: return gemv_m<8>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
   }
   return hipErrorInvalidValue;
 }
@@ -296,6 +419,164 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
         if (m < M) epilogue<EPI>(ea, m, n, acc[i][j][r]);
       }
     }
+}
+
+// ---- skinny MFMA GEMM (decode with M <= 64 rows per tile) --------------------
+//
+// Work-group tile 64 (M) x 16 (N), one 16x16 block per wave; operand fragments
+// go straight from global memory to registers (A rows are L2-resident and
+// shared by every work-group, each weight row is read once), eight k-steps
+// of 32 in flight per lane.  RMS: the row scale is computed in-kernel from
+// the same rows.  ksplit > 1 splits K over blockIdx.z; each split writes its
+// partial tile with coherent (sc1) stores and the last split to arrive sums
+// them in split order (deterministic) and runs the epilogue.
+
+constexpr int SK_D = 8;
+
+template <int EPI, bool RMS>
+__global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, int lda,
+                                                 const bf16_t* __restrict__ W, int M, int N, int K,
+                                                 int ksplit, float eps, EpiArgs ea,
+                                                 float* __restrict__ part,
+                                                 unsigned* __restrict__ cnt) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 64 + wv * 16, sidx = blockIdx.z;
+  const int kper = K / ksplit, kb = sidx * kper;
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  const int arow = m0 + r16, wrow = n0 + r16;
+  const bool aok = arow < M, wok = wrow < N;
+  const bf16_t* ap = A + (size_t)(aok ? arow : 0) * lda + kb + kq;
+  const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + kb + kq;
+  const int nsteps = kper >> 5;
+
+  float scale = 1.f;
+  if (RMS) {
+    float ss = 0.f;
+    for (int k = 0; k < K; k += 32) {
+      float f[8];
+      unpack8(aok ? *(const uint4*)(A + (size_t)arow * lda + k + kq) : make_uint4(0, 0, 0, 0), f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    scale = rsqrtf(ss / (float)K + eps);
+  }
+
+  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+  uint4 ca[SK_D], cw[SK_D], na[SK_D], nw[SK_D];
+#pragma unroll
+  for (int i = 0; i < SK_D; ++i) {
+    const bool ok = i < nsteps;
+    ca[i] = (ok && aok) ? *(const uint4*)(ap + i * 32) : make_uint4(0, 0, 0, 0);
+    cw[i] = (ok && wok) ? *(const uint4*)(wp + i * 32) : make_uint4(0, 0, 0, 0);
+  }
+  for (int s0 = 0; s0 < nsteps; s0 += SK_D) {
+    const bool more = s0 + SK_D < nsteps;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < SK_D; ++i) {
+        const bool ok = s0 + SK_D + i < nsteps;
+        na[i] = (ok && aok) ? *(const uint4*)(ap + (s0 + SK_D + i) * 32) : make_uint4(0, 0, 0, 0);
+        nw[i] = (ok && wok) ? *(const uint4*)(wp + (s0 + SK_D + i) * 32) : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i) {
+      if (s0 + i < nsteps) {
+        uint4 a = ca[i];
+        if (RMS) {
+          float f[8];
+          unpack8(a, f);
+          a.x = pack2(f[0] * scale, f[1] * scale);
+          a.y = pack2(f[2] * scale, f[3] * scale);
+          a.z = pack2(f[4] * scale, f[5] * scale);
+          a.w = pack2(f[6] * scale, f[7] * scale);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(bf16x8_t*)&a, *(bf16x8_t*)&cw[i], acc, 0,
+                                                      0, 0);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < SK_D; ++i) {
+        ca[i] = na[i];
+        cw[i] = nw[i];
+      }
+    }
+  }
+
+  const int n = n0 + r16;
+  if (ksplit == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + (lane >> 4) * 4 + r;
+      if (m < M && n < N) epilogue<EPI>(ea, m, n, acc[r]);
+    }
+    return;
+  }
+  // split-K: coherent partial stores, last arrival reduces in split order
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  float* pt = part + (size_t)tile * ksplit * 1024;
+  const int lr = wv * 16 + (lane >> 4) * 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    __hip_atomic_store(pt + (size_t)sidx * 1024 + (lr + r) * 16 + r16, acc[r], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ unsigned s_last;
+  if (tid == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (unsigned)ksplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = 0.f;
+    for (int sp = 0; sp < ksplit; ++sp)
+      v += __hip_atomic_load(pt + (size_t)sp * 1024 + (lr + r) * 16 + r16, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    const int m = m0 + (lane >> 4) * 4 + r;
+    if (m < M && n < N) epilogue<EPI>(ea, m, n, v);
+  }
+  if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int gemm_sk_split(int M, int N, int K) {
+  // enough work-groups to cover the GPU, each K slice a multiple of 32
+  const int tiles = ((N + 15) / 16) * ((M + 63) / 64);
+  int s = 1;
+  while (tiles * s < 192 && K % (64 * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
+  return s;
+}
+
+hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
+                       int K, float eps, const EpiArgs& ea, float* part, unsigned* cnt,
+                       hipStream_t st) {
+  if (K % 32 || M <= 0) return hipErrorInvalidValue;
+  const int ks = rms ? 1 : gemm_sk_split(M, N, K);
+  dim3 grid((N + 15) / 16, (M + 63) / 64, ks);
+#define ANN_SK(E)                                                                            \
+  if (rms)                                                                                   \
+    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ks,  \
+                       eps, ea, part, cnt);                                                  \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ks, \
+                       eps, ea, part, cnt);                                                  \
+  break;
+  switch (epi) {
+    case EPI_STORE: ANN_SK(EPI_STORE)
+    case EPI_RELU2: ANN_SK(EPI_RELU2)
+    case EPI_RESID_ATTN: ANN_SK(EPI_RESID_ATTN)
+    case EPI_RESID_MLP: ANN_SK(EPI_RESID_MLP)
+    case EPI_LOGITS: ANN_SK(EPI_LOGITS)
+    default: return hipErrorInvalidValue;
+  }
+#undef ANN_SK
+  return hipGetLastError();
 }
 
 hipError_t gemm(int epi, const bf16_t* A, int lda, const float* rs, const bf16_t* W, int M, int N,

@@ -69,9 +69,13 @@ __device__ int select_bin(const uint32_t* hist, uint32_t need, uint32_t* above) 
 }
 
 __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
-                                                        int Vs, float temperature, int top_k,
-                                                        uint64_t seed, uint64_t step,
-                                                        int32_t* __restrict__ out_tok) {
+                                                        int Vs, const SampParams* __restrict__ sp,
+                                                        unsigned long long* __restrict__ steps,
+                                                        int32_t* __restrict__ out_tok,
+                                                        int32_t* __restrict__ pos, int pos_adv) {
+  const float temperature = sp->temperature;
+  const int top_k = sp->top_k;
+  const uint64_t seed = sp->seed;
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
   __shared__ float s_sum[SMP_THREADS];
@@ -92,6 +96,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
       uint64_t b = 0;
       for (int w = 0; w < SMP_THREADS / 64; ++w) b = s_red[w] > b ? s_red[w] : b;
       out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+      if (pos) pos[row] += pos_adv;
     }
     return;
   }
@@ -169,6 +174,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   }
   const float total = s_sum[SMP_THREADS - 1];
   const float before = tid ? s_sum[tid - 1] : 0.f;
+  const uint64_t step = steps[row];
   const uint32_t w = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
                               (uint32_t)seed, (uint32_t)(seed >> 32));
   const float target = (float)(w >> 8) * (1.0f / 16777216.0f) * total;
@@ -196,7 +202,20 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
         if (softcap(bf2f(z[i])) / tmp >= zthr) { pick = (uint32_t)i; break; }
     }
     out_tok[row] = (int32_t)pick;
+    if (pos) pos[row] += pos_adv;
+    steps[row] = step + 1;
   }
+}
+
+__global__ void k_set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
+                               int top_k, unsigned long long seed, unsigned long long step) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) {
+    sp->temperature = temperature;
+    sp->top_k = top_k;
+    sp->seed = seed;
+  }
+  if (i < B) steps[i] = step;
 }
 
 __global__ void k_set_pos(int32_t* pos, int B, int value) {
@@ -209,10 +228,19 @@ __global__ void k_advance_pos(int32_t* pos, int B, int n) {
   if (i < B) pos[i] += n;
 }
 
-hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, float temperature, int top_k,
-                  uint64_t seed, uint64_t step, int32_t* out_tok, hipStream_t st) {
-  hipLaunchKernelGGL(k_sample, dim3(B), dim3(SMP_THREADS), 0, st, z, ldz, Vs, temperature, top_k,
-                     seed, step, out_tok);
+hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
+                  unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
+                  hipStream_t st) {
+  hipLaunchKernelGGL(k_sample, dim3(B), dim3(SMP_THREADS), 0, st, z, ldz, Vs, sp, steps, out_tok,
+                     pos, pos_adv);
+  return hipGetLastError();
+}
+
+hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
+                        int top_k, unsigned long long seed, unsigned long long step,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(k_set_sampling, dim3((B + 255) / 256), dim3(256), 0, st, sp, steps, B,
+                     temperature, top_k, seed, step);
   return hipGetLastError();
 }
 

@@ -102,7 +102,7 @@ def test_rms_kernel():
 # ---- whole forward -------------------------------------------------------------
 
 @pytest.mark.parametrize("name", ["dh64", "dh128"])
-@pytest.mark.parametrize("B,T", [(1, 5), (2, 40), (3, 1)])
+@pytest.mark.parametrize("B,T", [(1, 5), (2, 40), (3, 1), (3, 12)])
 def test_forward_logits_parity(name, B, T):
     cfg = small_cfgs()[name]
     p = perturb_lambdas(init_params(cfg, 11, dense=True))
@@ -116,13 +116,14 @@ def test_forward_logits_parity(name, B, T):
     assert torch.all((got > 0) & (got < 23))
 
 
-@pytest.mark.parametrize("name", ["dh64", "dh128"])
-def test_decode_teacher_forced_past_window(name):
+@pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 12)])
+def test_decode_teacher_forced_past_window(name, B):
     """Decode logits at every position (well past the window) match the
-    oracle's KV-cache forward on the same tokens."""
+    oracle's KV-cache forward on the same tokens (B=12 takes the skinny MFMA
+    GEMM and the split-combine kernel instead of the GEMV)."""
     cfg = small_cfgs()[name]
     p = perturb_lambdas(init_params(cfg, 5, dense=True))
-    B, T0, steps = 2, 7, cfg.seq_len - 7
+    T0, steps = 7, cfg.seq_len - 7
     tok = np.random.default_rng(1).integers(0, cfg.vocab_size, (B, T0 + steps))
     eng = _engine(cfg, p, B)
     prep = R.Prepared(cfg, p)
