@@ -198,10 +198,17 @@ __global__ void k_attn_dec_combine(const float* __restrict__ part, bf16_t* __res
                                    int H, int nsplit) {
   const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const float* pp = part + ((size_t)b * H + h) * nsplit * (DH + 1);
+  float v[32], w[32];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {   // nsplit <= 32: every load in flight at once
+    v[s] = s < nsplit ? pp[s * (DH + 1) + t] : 0.f;
+    w[s] = s < nsplit ? pp[s * (DH + 1) + DH] : 0.f;
+  }
   float o = 0.f, l = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    o += pp[s * (DH + 1) + t];
-    l += pp[s * (DH + 1) + DH];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {
+    o += v[s];
+    l += w[s];
   }
   out[(size_t)b * H * DH + h * DH + t] = f2bf(o / l);
 }

@@ -204,18 +204,21 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
          int M, int N, int K, EpiArgs ea, hipStream_t st, PreArgs pa = PreArgs{}) {
   float* rs = nullptr;
   const bool use_gemv = gemv_fits(M, K);
+  // the skinny GEMM re-reads A per 16 columns: wide outputs (lm_head) go to
+  // the 128x128 GEMM
+  const bool use_sk = !use_gemv && M <= 64 && N <= 8 * K &&
+                      (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <= SK_PART_FLOATS;
   if (pre == PRE_ATTN && !use_gemv) return fail(ANN_E_ARG, "attention prologue needs the GEMV");
-  if (pre == PRE_RMS && !use_gemv && M > 64) {
+  if (pre == PRE_RMS && !use_gemv) {
     rs = c->sp<float>(c->sl.rs);
     HIPCHK(row_rms_scale(X, ldx, rs, M, K, c->c.rms_eps, st));
   }
   ProfScope ps(c, kind, st);
   if (use_gemv)
     HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, pa, st));
-  else if (M <= 64 && (pre == PRE_RMS || (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <=
-                                              SK_PART_FLOATS))
-    HIPCHK(gemm_skinny(epi, pre == PRE_RMS, X, ldx, W, M, N, K, c->c.rms_eps, ea,
-                       c->sp<float>(c->sl.skpart), c->sp<unsigned>(c->sl.skcnt), st));
+  else if (use_sk)
+    HIPCHK(gemm_skinny(epi, rs, X, ldx, W, M, N, K, ea, c->sp<float>(c->sl.skpart),
+                       c->sp<unsigned>(c->sl.skcnt), st));
   else
     HIPCHK(gemm(epi, X, ldx, rs, W, M, N, K, ea, st));
   return ANN_OK;

@@ -90,20 +90,36 @@ __global__ void k_embed_rms(const int32_t* __restrict__ tok, const bf16_t* __res
   }
 }
 
-// Row scale s_m = rsqrt(mean(x_m^2) + eps) for the GEMM RMS prologue.
-__global__ void k_row_rms_scale(const bf16_t* __restrict__ x, int ldx, float* __restrict__ s,
-                                int M, int d, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (m >= M) return;
-  const bf16_t* r = x + (size_t)m * ldx;
-  float ss = 0.f;
-  for (int i = lane; i < d; i += 64) {
-    float v = bf2f(r[i]);
-    ss += v * v;
+// Row scale s_m = rsqrt(mean(x_m^2) + eps) for the GEMM RMS prologue.  One
+// work-group per row; every 16-byte chunk of the row is loaded up front.
+__global__ __launch_bounds__(256) void k_row_rms_scale(const bf16_t* __restrict__ x, int ldx,
+                                                       float* __restrict__ s, int d, float eps) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const uint4* r = (const uint4*)(x + (size_t)m * ldx);
+  const int K8 = d >> 3;
+  uint4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = tid + u * 256;
+    v[u] = c < K8 ? r[c] : make_uint4(0, 0, 0, 0);
   }
-  ss = group_sum<64>(ss);
-  if (lane == 0) s[m] = rsqrtf(ss / (float)d + eps);
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float f[8];
+    unpack8(v[u], f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  }
+  for (int c = tid + 1024; c < K8; c += 256) {   // rows longer than 8192
+    float f[8];
+    unpack8(r[c], f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  }
+  const float t = block_sum(ss, red);
+  if (tid == 0) s[m] = rsqrtf(t / (float)d + eps);
 }
 
 // ---- QK-norm + RoPE + KV-cache append --------------------------------------
@@ -256,7 +272,7 @@ hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x
 
 hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
                          hipStream_t st) {
-  hipLaunchKernelGGL(k_row_rms_scale, dim3(cdiv(M, 4)), dim3(256), 0, st, x, ldx, s, M, d, eps);
+  hipLaunchKernelGGL(k_row_rms_scale, dim3(M), dim3(256), 0, st, x, ldx, s, d, eps);
   return hipGetLastError();
 }
 

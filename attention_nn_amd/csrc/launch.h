@@ -71,11 +71,11 @@ bool gemv_fits(int M, int K);
 int gemv_blocks(int N, int K);
 hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
                            int32_t* pos, int pos_adv, hipStream_t st);
-// Skinny MFMA GEMM for decode (M small, N moderate): y = (rms?)(A) @ W^T;
+// Skinny MFMA GEMM for decode (M small, N moderate): y = (rs_m * A) @ W^T;
 // part / cnt: split-K scratch (tiles * ksplit * 1024 floats, tiles counters,
 // counters zero between calls).
-hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
-                       int K, float eps, const EpiArgs& ea, float* part, unsigned* cnt,
+hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const bf16_t* W, int M,
+                       int N, int K, const EpiArgs& ea, float* part, unsigned* cnt,
                        hipStream_t st);
 int gemm_sk_split(int M, int N, int K);
 // MFMA GEMM: y = (rs_m * A) @ W^T with A (M, lda) bf16; rs null = no scaling.

@@ -56,30 +56,26 @@ __device__ __forceinline__ void gemv_prologue(uint4* xs4, const bf16_t* __restri
   const int tid = threadIdx.x;
   const int K8 = K >> 3;
   if (PRE == PRE_ATTN) {
-    // o[m][h*Dh + e] = sum_s O_s / sum_s L_s, rounded to bf16
+    // o[m][h*Dh + e] = sum_s O_s / sum_s L_s, rounded once to bf16; nsplit
+    // <= 32, every split's O and L loads issued before any is consumed
     const int Dh = pa.Dh, ns = pa.nsplit, st = Dh + 1, H = pa.H;
-    float* linv = red;   // M * H reciprocals of sum_s L_s (M * H <= 8 * 16)
-    for (int i = tid; i < M * H; i += GEMV_THREADS) {
-      const float* pp = pa.part + (size_t)i * ns * st + Dh;
-      float l = 0.f;
-      for (int s = 0; s < ns; ++s) l += pp[s * st];
-      linv[i] = 1.f / l;
-    }
-    __syncthreads();
     bf16_t* xs = (bf16_t*)xs4;
     for (int i = tid; i < M * K; i += GEMV_THREADS) {
       const int m = i / K, k = i % K, h = k / Dh, e = k % Dh;
-      const float* pp = pa.part + ((size_t)m * H + h) * ns * st + e;
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-      int s = 0;
-      for (; s + 4 <= ns; s += 4) {
-        o0 += pp[s * st];
-        o1 += pp[(s + 1) * st];
-        o2 += pp[(s + 2) * st];
-        o3 += pp[(s + 3) * st];
+      const float* pp = pa.part + ((size_t)m * H + h) * ns * st;
+      float v[32], l[32];
+#pragma unroll
+      for (int s = 0; s < 32; ++s) {
+        v[s] = s < ns ? pp[s * st + e] : 0.f;
+        l[s] = s < ns ? pp[s * st + Dh] : 0.f;
       }
-      for (; s < ns; ++s) o0 += pp[s * st];
-      xs[i] = f2bf(((o0 + o1) + (o2 + o3)) * linv[m * H + h]);
+      float o = 0.f, L = 0.f;
+#pragma unroll
+      for (int s = 0; s < 32; ++s) {
+        o += v[s];
+        L += l[s];
+      }
+      xs[i] = f2bf(o / L);
     }
     return;
   }
@@ -426,8 +422,8 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
 // Work-group tile 64 (M) x 16 (N), one 16x16 block per wave; operand fragments
 // go straight from global memory to registers (A rows are L2-resident and
 // shared by every work-group, each weight row is read once), eight k-steps
-// of 32 in flight per lane.  RMS: the row scale is computed in-kernel from
-// the same rows.  ksplit > 1 splits K over blockIdx.z; each split writes its
+// of 32 in flight per lane.  RMS: A rows are scaled by rs[m] and rounded to
+// bf16 as they are loaded.  ksplit > 1 splits K over blockIdx.z; each split writes its
 // partial tile with coherent (sc1) stores and the last split to arrive sums
 // them in split order (deterministic) and runs the epilogue.
 
@@ -435,8 +431,9 @@ constexpr int SK_D = 8;
 
 template <int EPI, bool RMS>
 __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, int lda,
+                                                 const float* __restrict__ rs,
                                                  const bf16_t* __restrict__ W, int M, int N, int K,
-                                                 int ksplit, float eps, EpiArgs ea,
+                                                 int ksplit, EpiArgs ea,
                                                  float* __restrict__ part,
                                                  unsigned* __restrict__ cnt) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -449,19 +446,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
   const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + kb + kq;
   const int nsteps = kper >> 5;
 
-  float scale = 1.f;
-  if (RMS) {
-    float ss = 0.f;
-    for (int k = 0; k < K; k += 32) {
-      float f[8];
-      unpack8(aok ? *(const uint4*)(A + (size_t)arow * lda + k + kq) : make_uint4(0, 0, 0, 0), f);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
-    }
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
-    scale = rsqrtf(ss / (float)K + eps);
-  }
+  const float scale = (RMS && aok) ? rs[arow] : 1.f;
 
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
   uint4 ca[SK_D], cw[SK_D], na[SK_D], nw[SK_D];
@@ -553,19 +538,20 @@ int gemm_sk_split(int M, int N, int K) {
   return s;
 }
 
-hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
-                       int K, float eps, const EpiArgs& ea, float* part, unsigned* cnt,
+hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const bf16_t* W, int M,
+                       int N, int K, const EpiArgs& ea, float* part, unsigned* cnt,
                        hipStream_t st) {
   if (K % 32 || M <= 0) return hipErrorInvalidValue;
-  const int ks = rms ? 1 : gemm_sk_split(M, N, K);
+  const bool rms = rs != nullptr;
+  const int ks = gemm_sk_split(M, N, K);
   dim3 grid((N + 15) / 16, (M + 63) / 64, ks);
 #define ANN_SK(E)                                                                            \
   if (rms)                                                                                   \
-    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ks,  \
-                       eps, ea, part, cnt);                                                  \
+    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, rs, W, M, N, K,  \
+                       ks, ea, part, cnt);                                                   \
   else                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ks, \
-                       eps, ea, part, cnt);                                                  \
+    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, \
+                       ks, ea, part, cnt);                                                   \
   break;
   switch (epi) {
     case EPI_STORE: ANN_SK(EPI_STORE)

@@ -68,6 +68,24 @@ __device__ int select_bin(const uint32_t* hist, uint32_t need, uint32_t* above) 
   return 0;
 }
 
+constexpr int SMP_CH = 7;  // 16-byte chunks per thread: 1024 * 56 >= 50257
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
+  v = wave_max_u64(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  uint64_t b = 0;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) b = red[w] > b ? red[w] : b;
+  return b;
+}
+
+// One work-group per row; thread t holds the contiguous slice
+// [56 t, 56 t + 56) of the row in registers, so the row is read from memory
+// once and every pass (radix select, max, weights, scan, draw) runs on
+// registers and LDS.
 __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
                                                         int Vs, const SampParams* __restrict__ sp,
                                                         unsigned long long* __restrict__ steps,
@@ -78,36 +96,49 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   const uint64_t seed = sp->seed;
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
-  __shared__ float s_sum[SMP_THREADS];
+  __shared__ float s_wsum[SMP_THREADS / 64];
   __shared__ uint32_t s_misc[4];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const bf16_t* z = zall + (size_t)row * ldz;
+  const int base = tid * SMP_CH * 8;
+
+  uint4 raw[SMP_CH];
+#pragma unroll
+  for (int c = 0; c < SMP_CH; ++c)
+    raw[c] = (base + c * 8 < ldz) ? *(const uint4*)(z + base + c * 8) : make_uint4(0, 0, 0, 0);
+  auto elem = [&](int i) -> bf16_t {   // i in [0, 56)
+    const uint4& w = raw[i >> 3];
+    const uint32_t word = (i & 7) < 2 ? w.x : (i & 7) < 4 ? w.y : (i & 7) < 6 ? w.z : w.w;
+    return (bf16_t)((i & 1) ? (word >> 16) : (word & 0xffffu));
+  };
 
   if (temperature == 0.f) {
     uint64_t best = 0;
-    for (int i = tid; i < Vs; i += SMP_THREADS) {
-      const uint64_t key = ((uint64_t)okey(z[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-      best = key > best ? key : best;
+#pragma unroll
+    for (int i = 0; i < SMP_CH * 8; ++i) {
+      const int gi = base + i;
+      if (gi < Vs) {
+        const uint64_t key = ((uint64_t)okey(elem(i)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)gi);
+        best = key > best ? key : best;
+      }
     }
-    best = wave_max_u64(best);
-    if (lane == 0) s_red[wv] = best;
-    __syncthreads();
+    best = block_max_u64(best, s_red);
     if (tid == 0) {
-      uint64_t b = 0;
-      for (int w = 0; w < SMP_THREADS / 64; ++w) b = s_red[w] > b ? s_red[w] : b;
-      out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+      out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
       if (pos) pos[row] += pos_adv;
     }
     return;
   }
 
-  // ---- k-th largest 16-bit key (exact), or the minimum when keeping all
+  // ---- k-th largest 16-bit key (exact) when top-k applies
   uint32_t thr_key = 0;
   const bool use_thr = top_k > 0 && top_k < Vs;
   if (use_thr) {
     for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < Vs; i += SMP_THREADS) atomicAdd(&hist[okey(z[i]) >> 8], 1u);
+#pragma unroll
+    for (int i = 0; i < SMP_CH * 8; ++i)
+      if (base + i < Vs) atomicAdd(&hist[okey(elem(i)) >> 8], 1u);
     __syncthreads();
     if (tid == 0) {
       uint32_t above;
@@ -119,9 +150,10 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     const uint32_t b1 = s_misc[0];
     for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < Vs; i += SMP_THREADS) {
-      const uint32_t k = okey(z[i]);
-      if ((k >> 8) == b1) atomicAdd(&hist[k & 0xffu], 1u);
+#pragma unroll
+    for (int i = 0; i < SMP_CH * 8; ++i) {
+      const uint32_t k = okey(elem(i));
+      if (base + i < Vs && (k >> 8) == b1) atomicAdd(&hist[k & 0xffu], 1u);
     }
     __syncthreads();
     if (tid == 0) {
@@ -135,19 +167,10 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
 
   // ---- threshold and maximum in the softcapped / tempered domain
   uint32_t kmax = 0;
-  for (int i = tid; i < Vs; i += SMP_THREADS) kmax = max(kmax, okey(z[i]));
-  {
-    uint64_t v = wave_max_u64(kmax);
-    if (lane == 0) s_red[wv] = v;
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t b = 0;
-      for (int w = 0; w < SMP_THREADS / 64; ++w) b = s_red[w] > b ? s_red[w] : b;
-      s_misc[3] = (uint32_t)b;
-    }
-    __syncthreads();
-    kmax = s_misc[3];
-  }
+#pragma unroll
+  for (int i = 0; i < SMP_CH * 8; ++i)
+    if (base + i < Vs) kmax = max(kmax, okey(elem(i)));
+  kmax = (uint32_t)block_max_u64(kmax, s_red);
   auto key2bf = [](uint32_t k) -> bf16_t {
     return (bf16_t)((k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu));
   };
@@ -155,53 +178,68 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   const float zmax = softcap(bf2f(key2bf(kmax))) / tmp;
   const float zthr = use_thr ? softcap(bf2f(key2bf(thr_key))) / tmp : -INFINITY;
 
-  // ---- contiguous segment per thread, deterministic scan
-  const int seg = (Vs + SMP_THREADS - 1) / SMP_THREADS;
-  const int i0 = min(Vs, tid * seg), i1 = min(Vs, i0 + seg);
+  // ---- weights of this thread's slice, block exclusive scan (fixed order)
   float local = 0.f;
-  for (int i = i0; i < i1; ++i) {
-    const float zc = softcap(bf2f(z[i])) / tmp;
-    if (zc >= zthr) local += expf(zc - zmax);
+#pragma unroll
+  for (int i = 0; i < SMP_CH * 8; ++i) {
+    if (base + i < Vs) {
+      const float zc = softcap(bf2f(elem(i))) / tmp;
+      if (zc >= zthr) local += expf(zc - zmax);
+    }
   }
-  s_sum[tid] = local;
+  float incl = local;   // inclusive scan within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) s_wsum[wv] = incl;
   __syncthreads();
-  // Hillis-Steele inclusive scan over SMP_THREADS values (fixed order)
-  for (int off = 1; off < SMP_THREADS; off <<= 1) {
-    const float v = tid >= off ? s_sum[tid - off] : 0.f;
-    __syncthreads();
-    s_sum[tid] += v;
-    __syncthreads();
+  float wbase = 0.f, total = 0.f;
+  for (int w = 0; w < SMP_THREADS / 64; ++w) {
+    if (w < wv) wbase += s_wsum[w];
+    total += s_wsum[w];
   }
-  const float total = s_sum[SMP_THREADS - 1];
-  const float before = tid ? s_sum[tid - 1] : 0.f;
+  const float before = wbase + incl - local;
   const uint64_t step = steps[row];
-  const uint32_t w = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
-                              (uint32_t)seed, (uint32_t)(seed >> 32));
-  const float target = (float)(w >> 8) * (1.0f / 16777216.0f) * total;
+  const uint32_t rw = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
+                               (uint32_t)seed, (uint32_t)(seed >> 32));
+  const float target = (float)(rw >> 8) * (1.0f / 16777216.0f) * total;
   if (tid == 0) s_misc[0] = 0xffffffffu;
   __syncthreads();
-  if (target >= before && target < before + local) {
+  if (local > 0.f && target >= before && target < before + local) {
     float run = before;
     int pick = -1, last = -1;
-    for (int i = i0; i < i1; ++i) {
-      const float zc = softcap(bf2f(z[i])) / tmp;
-      if (zc >= zthr) {
-        last = i;
-        run += expf(zc - zmax);
-        if (target < run) { pick = i; break; }
+#pragma unroll
+    for (int i = 0; i < SMP_CH * 8; ++i) {
+      if (pick < 0 && base + i < Vs) {
+        const float zc = softcap(bf2f(elem(i))) / tmp;
+        if (zc >= zthr) {
+          last = base + i;
+          run += expf(zc - zmax);
+          if (target < run) pick = base + i;
+        }
       }
     }
     if (pick < 0) pick = last;
     atomicMin(&s_misc[0], (uint32_t)pick);
   }
   __syncthreads();
+  if (s_misc[0] == 0xffffffffu) {
+    // rounding put the target at/after the total: take the last kept index
+    int lastk = -1;
+#pragma unroll
+    for (int i = 0; i < SMP_CH * 8; ++i)
+      if (base + i < Vs && softcap(bf2f(elem(i))) / tmp >= zthr) lastk = base + i;
+    __syncthreads();
+    if (tid == 0) s_misc[2] = 0;
+    __syncthreads();
+    if (lastk >= 0) atomicMax(&s_misc[2], (uint32_t)lastk);
+    __syncthreads();
+    if (tid == 0) s_misc[0] = s_misc[2];
+  }
   if (tid == 0) {
-    uint32_t pick = s_misc[0];
-    if (pick == 0xffffffffu) {  // rounding put target at/after the total: last kept index
-      for (int i = Vs - 1; i >= 0; --i)
-        if (softcap(bf2f(z[i])) / tmp >= zthr) { pick = (uint32_t)i; break; }
-    }
-    out_tok[row] = (int32_t)pick;
+    out_tok[row] = (int32_t)s_misc[0];
     if (pos) pos[row] += pos_adv;
     steps[row] = step + 1;
   }
