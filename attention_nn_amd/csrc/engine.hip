@@ -284,8 +284,8 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
                       g.rms_eps, st));
       {
         ProfScope ps(c, ANN_PROF_ATTN, st);
-        HIPCHK(attention(q, c->kcache(l), c->vcache(l), pos, ao, part, M, T, H, Dh, g.max_ctx,
-                         g.window, lng, g.attn_scale, 1, st));
+        HIPCHK(attn_prefill(q, c->kcache(l), c->vcache(l), pos, ao, B, T, H, Dh, g.max_ctx,
+                            g.window, lng, g.attn_scale, st));
       }
       rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d, d,
                 er, st);

@@ -89,6 +89,12 @@ hipError_t attention(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const 
                      bf16_t* out, float* part, int M, int T, int H, int Dh, int max_ctx,
                      int window, bool long_layer, float scale, int nsplit, hipStream_t st);
 
+// Prefill attention (MFMA flash attention) of B x T query rows at positions
+// pos[b] + t against keys [window start, own position] of the cache.
+hipError_t attn_prefill(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const int32_t* pos,
+                        bf16_t* out, int B, int T, int H, int Dh, int max_ctx, int window,
+                        bool long_layer, float scale, hipStream_t st);
+
 // Decode attention with fused QK-norm / RoPE / KV append (one token per
 // sequence); writes split partials (B, H, nsplit, Dh + 1).
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
