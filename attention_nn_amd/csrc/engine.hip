@@ -74,7 +74,7 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, skcnt, skpart, x, x0, qkv, q, ao, hid, rs, part, zb, total;
+  size_t pos, sp, steps, amax, skcnt, skpart, x, x0, qkv, q, ao, hn, hid, rs, part, zb, total;
 };
 constexpr int SK_MAX_TILES = 4096;          // split-K counters of the skinny GEMM
 constexpr size_t SK_PART_FLOATS = 512 * 1024;  // split-K partial tiles (<= 512 of 1024)
@@ -94,6 +94,7 @@ SLayout ws_layout(const ann_config& c) {
   s.qkv = off; off += up(M * 3 * d * 2);
   s.q = off; off += up(M * d * 2);
   s.ao = off; off += up(M * d * 2);
+  s.hn = off; off += up(M * d * 2);
   s.hid = off; off += up(M * 4 * d * 2);
   s.rs = off; off += up(M * 4);
   s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
@@ -202,16 +203,22 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
 // y = pre(X) @ W^T for M rows with the given epilogue.
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st, PreArgs pa = PreArgs{}) {
-  float* rs = nullptr;
   const bool use_gemv = gemv_fits(M, K);
   // the skinny GEMM re-reads A per 16 columns: wide outputs (lm_head) go to
-  // the 128x128 GEMM
+  // the large-tile GEMM
   const bool use_sk = !use_gemv && M <= 64 && N <= 8 * K &&
                       (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <= SK_PART_FLOATS;
   if (pre == PRE_ATTN && !use_gemv) return fail(ANN_E_ARG, "attention prologue needs the GEMV");
-  if (pre == PRE_RMS && !use_gemv) {
+  float* rs = nullptr;
+  if (pre == PRE_RMS && use_sk) {   // row scales applied as the skinny GEMM loads A
     rs = c->sp<float>(c->sl.rs);
     HIPCHK(row_rms_scale(X, ldx, rs, M, K, c->c.rms_eps, st));
+  } else if (pre == PRE_RMS && !use_gemv) {   // large GEMM: A normalised once into h
+    if (K > c->c.d) return fail(ANN_E_ARG, "RMS prologue wider than the model dim");
+    bf16_t* h = c->sp<bf16_t>(c->sl.hn);
+    HIPCHK(rms_apply(X, ldx, h, K, M, K, c->c.rms_eps, st));
+    X = h;
+    ldx = K;
   }
   ProfScope ps(c, kind, st);
   if (use_gemv)
@@ -220,7 +227,7 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
     HIPCHK(gemm_skinny(epi, rs, X, ldx, W, M, N, K, ea, c->sp<float>(c->sl.skpart),
                        c->sp<unsigned>(c->sl.skcnt), st));
   else
-    HIPCHK(gemm(epi, X, ldx, rs, W, M, N, K, ea, st));
+    HIPCHK(gemm(epi, X, ldx, W, M, N, K, ea, st));
   return ANN_OK;
 }
 

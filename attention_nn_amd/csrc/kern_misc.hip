@@ -122,6 +122,47 @@ __global__ __launch_bounds__(256) void k_row_rms_scale(const bf16_t* __restrict_
   if (tid == 0) s[m] = rsqrtf(t / (float)d + eps);
 }
 
+// h = bf16(x * rsqrt(mean(x^2) + eps)) (model.py:49 with the bf16 output of
+// an eager op); one work-group per row, every chunk loaded up front.
+__global__ __launch_bounds__(256) void k_rms_apply(const bf16_t* __restrict__ x, int ldx,
+                                                   bf16_t* __restrict__ h, int ldh, int d,
+                                                   float eps) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const uint4* r = (const uint4*)(x + (size_t)m * ldx);
+  uint4* o = (uint4*)(h + (size_t)m * ldh);
+  const int K8 = d >> 3;
+  uint4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = tid + u * 256;
+    v[u] = c < K8 ? r[c] : make_uint4(0, 0, 0, 0);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float f[8];
+    unpack8(v[u], f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  }
+  const float s = rsqrtf(block_sum(ss, red) / (float)d + eps);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = tid + u * 256;
+    if (c < K8) {
+      float f[8];
+      unpack8(v[u], f);
+      uint4 w;
+      w.x = pack2(f[0] * s, f[1] * s);
+      w.y = pack2(f[2] * s, f[3] * s);
+      w.z = pack2(f[4] * s, f[5] * s);
+      w.w = pack2(f[6] * s, f[7] * s);
+      o[c] = w;
+    }
+  }
+}
+
 // ---- QK-norm + RoPE + KV-cache append --------------------------------------
 
 // qkv (M, 3*H*Dh) bf16 -> q (M, H*Dh) = rope(rms(q)); K/V cache rows written
@@ -273,6 +314,13 @@ hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x
 hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
                          hipStream_t st) {
   hipLaunchKernelGGL(k_row_rms_scale, dim3(M), dim3(256), 0, st, x, ldx, s, d, eps);
+  return hipGetLastError();
+}
+
+hipError_t rms_apply(const bf16_t* x, int ldx, bf16_t* h, int ldh, int M, int d, float eps,
+                     hipStream_t st) {
+  if (d > 8192 || d % 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rms_apply, dim3(M), dim3(256), 0, st, x, ldx, h, ldh, d, eps);
   return hipGetLastError();
 }
 

@@ -78,9 +78,12 @@ hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const
                        int N, int K, const EpiArgs& ea, float* part, unsigned* cnt,
                        hipStream_t st);
 int gemm_sk_split(int M, int N, int K);
-// MFMA GEMM: y = (rs_m * A) @ W^T with A (M, lda) bf16; rs null = no scaling.
-hipError_t gemm(int epi, const bf16_t* A, int lda, const float* rs, const bf16_t* W, int M,
-                int N, int K, const EpiArgs& ea, hipStream_t st);
+// MFMA GEMM (prefill): y = A @ W^T with A (M, lda) bf16.
+hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                const EpiArgs& ea, hipStream_t st);
+// h = bf16(rms(x)) for M rows of length d (row strides ldx / ldh).
+hipError_t rms_apply(const bf16_t* x, int ldx, bf16_t* h, int ldh, int M, int d, float eps,
+                     hipStream_t st);
 
 // Attention of M query rows (row m = token t = m % T of sequence b = m / T at
 // position pos[b] + t) against the KV cache.  nsplit > 1 splits each row's key

@@ -317,13 +317,17 @@ hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int
   return hipErrorInvalidValue;
 }
 
-// ---- MFMA GEMM --------------------------------------------------------------
+// ---- MFMA GEMM, large M (prefill) -------------------------------------------
+//
+// 128 x 128 x 64 block tiles, 4 waves of 64 x 64 (4 x 4 blocks of
+// v_mfma_f32_16x16x32_bf16), K tiles staged through padded LDS with the next
+// tile prefetched into registers during the MFMAs.  A arrives already
+// normalised (rms_apply) when the projection needs it.
 
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64, GM_LDS = GM_BK + 8;  // +16 B row pad
 
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int lda,
-                                              const float* __restrict__ rs,
                                               const bf16_t* __restrict__ W, int M, int N, int K,
                                               EpiArgs ea) {
   __shared__ __attribute__((aligned(16))) bf16_t As[GM_BM * GM_LDS];
@@ -334,7 +338,6 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
 
   // each thread moves 4 16-byte chunks of A and 4 of B per K tile
   int arow[4], acol[4];
-  float ascale[4];
   bool aok[4], bok[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -343,7 +346,6 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
     acol[i] = (id & 7) * 8;
     aok[i] = (m0 + arow[i]) < M;
     bok[i] = (n0 + arow[i]) < N;
-    ascale[i] = (rs && aok[i]) ? rs[m0 + arow[i]] : 1.f;
   }
   uint4 ra[4], rb[4];
   auto load_tile = [&](int k0) {
@@ -358,17 +360,7 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
   auto store_tile = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint4 v = ra[i];
-      if (rs) {
-        float f[8];
-        unpack8(v, f);
-        const float s = ascale[i];
-        v.x = pack2(f[0] * s, f[1] * s);
-        v.y = pack2(f[2] * s, f[3] * s);
-        v.z = pack2(f[4] * s, f[5] * s);
-        v.w = pack2(f[6] * s, f[7] * s);
-      }
-      *(uint4*)(As + arow[i] * GM_LDS + acol[i]) = v;
+      *(uint4*)(As + arow[i] * GM_LDS + acol[i]) = ra[i];
       *(uint4*)(Bs + arow[i] * GM_LDS + acol[i]) = rb[i];
     }
   };
@@ -565,25 +557,25 @@ hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const
   return hipGetLastError();
 }
 
-hipError_t gemm(int epi, const bf16_t* A, int lda, const float* rs, const bf16_t* W, int M, int N,
-                int K, const EpiArgs& ea, hipStream_t st) {
+hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                const EpiArgs& ea, hipStream_t st) {
   if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
   dim3 grid((N + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
   switch (epi) {
     case EPI_STORE:
-      hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, ea);
+      hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
       break;
     case EPI_RELU2:
-      hipLaunchKernelGGL(k_gemm<EPI_RELU2>, grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, ea);
+      hipLaunchKernelGGL(k_gemm<EPI_RELU2>, grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
       break;
     case EPI_RESID_ATTN:
-      hipLaunchKernelGGL(k_gemm<EPI_RESID_ATTN>, grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, ea);
+      hipLaunchKernelGGL(k_gemm<EPI_RESID_ATTN>, grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
       break;
     case EPI_RESID_MLP:
-      hipLaunchKernelGGL(k_gemm<EPI_RESID_MLP>, grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, ea);
+      hipLaunchKernelGGL(k_gemm<EPI_RESID_MLP>, grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
       break;
     case EPI_LOGITS:
-      hipLaunchKernelGGL(k_gemm<EPI_LOGITS>, grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, ea);
+      hipLaunchKernelGGL(k_gemm<EPI_LOGITS>, grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
       break;
     default:
       return hipErrorInvalidValue;
