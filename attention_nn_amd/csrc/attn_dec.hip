@@ -14,7 +14,10 @@
 // |s| <= scale * Dh = shift (host-checked <= 40), and exp(s - shift) lies in
 // [e^-2shift, ~1] -- no overflow, no underflow to 0 in fp32.  Splits are then
 // plain sums: O_s = sum_j e^(s_j - shift) v_j, L_s = sum_j e^(s_j - shift), and
-// the consumer forms o = sum_s O_s / sum_s L_s (rounded once to bf16).
+// o = sum_s O_s / sum_s L_s (rounded once to bf16) is formed by the last split
+// of (b, h) to finish: partials go out with coherent (sc1) stores, a device
+// counter per (b, h) elects that split, which reads them back in split order
+// (deterministic) and resets the counter.
 //
 // Chunk of 64 keys: 4 lanes x 64 B read one 256-B key row (Dh = 128); for
 // P.V 16 lanes x 16 B cover a V row, 16 key groups accumulate in registers
@@ -32,8 +35,8 @@ template <int DH>
 __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     const bf16_t* __restrict__ qkv, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
-    float* __restrict__ part, int H, int max_ctx, int window, int is_long, float scale,
-    float shift, float eps, int nsplit) {
+    float* __restrict__ part, unsigned* __restrict__ cnt, bf16_t* __restrict__ out, int H,
+    int max_ctx, int window, int is_long, float scale, float shift, float eps, int nsplit) {
   constexpr int TPK = AD_THREADS / AD_KC;   // threads per key in the score pass (4)
   constexpr int DPT = DH / TPK;             // dims per thread in the score pass
   constexpr int VL = DH / 8;                // lanes per V row (16-byte slices)
@@ -178,71 +181,70 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
   lsum = group_sum<64>(lsum);
   if ((tid & 63) == 0) s_l[tid >> 6] = lsum;
   __syncthreads();
-  float* pp = part + (((size_t)b * H + h) * nsplit + split) * (DH + 1);
+  // partial (O, L) of this split with coherent stores; the last split of
+  // (b, h) to arrive sums all of them in split order and writes o = O / L
+  float* pbase = part + ((size_t)b * H + h) * nsplit * (DH + 1);
+  float* pp = pbase + (size_t)split * (DH + 1);
   if (tid < DH) {
     float o = 0.f;
 #pragma unroll
     for (int g = 0; g < NG; ++g) o += s_o[g][tid];
-    pp[tid] = o;
+    __hip_atomic_store(pp + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (tid == 0) {
     float l = 0.f;
     for (int w = 0; w < AD_THREADS / 64; ++w) l += s_l[w];
-    pp[DH] = l;
+    __hip_atomic_store(pp + DH, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// o (B, H*DH) bf16 = sum_s O_s / sum_s L_s  (for the GEMM path of the O-proj).
-template <int DH>
-__global__ void k_attn_dec_combine(const float* __restrict__ part, bf16_t* __restrict__ out,
-                                   int H, int nsplit) {
-  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-  const float* pp = part + ((size_t)b * H + h) * nsplit * (DH + 1);
-  float v[32], w[32];
-#pragma unroll
-  for (int s = 0; s < 32; ++s) {   // nsplit <= 32: every load in flight at once
-    v[s] = s < nsplit ? pp[s * (DH + 1) + t] : 0.f;
-    w[s] = s < nsplit ? pp[s * (DH + 1) + DH] : 0.f;
+  if (nsplit == 1) {
+    __syncthreads();
+    if (tid < DH) {
+      const float o = __hip_atomic_load(pp + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float l = __hip_atomic_load(pp + DH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      out[(size_t)b * d + h * DH + tid] = f2bf(o / l);
+    }
+    return;
   }
-  float o = 0.f, l = 0.f;
-#pragma unroll
-  for (int s = 0; s < 32; ++s) {
-    o += v[s];
-    l += w[s];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ unsigned s_last;
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(cnt + b * H + h, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (unsigned)nsplit - 1;
   }
-  out[(size_t)b * H * DH + h * DH + t] = f2bf(o / l);
+  __syncthreads();
+  if (!s_last) return;
+  if (tid < DH) {
+    float o = 0.f, l = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      o += __hip_atomic_load(pbase + (size_t)sp * (DH + 1) + tid, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      l += __hip_atomic_load(pbase + (size_t)sp * (DH + 1) + DH, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+    out[(size_t)b * d + h * DH + tid] = f2bf(o / l);
+  }
+  if (tid == 0) __hip_atomic_store(cnt + b * H + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
-                       const float* cs, const float* sn, float* part, int B, int H, int Dh,
-                       int max_ctx, int window, bool long_layer, float scale, float eps,
-                       int nsplit, hipStream_t st) {
+                       const float* cs, const float* sn, float* part, unsigned* cnt, bf16_t* out,
+                       int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
+                       float eps, int nsplit, hipStream_t st) {
   if (nsplit < 1 || B <= 0) return hipErrorInvalidValue;
   const float shift = scale * (float)Dh * 1.02f;
   dim3 grid(nsplit, H, B);
   switch (Dh) {
     case 64:
       hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
-                         part, H, max_ctx, window, (int)long_layer, scale, shift, eps, nsplit);
+                         part, cnt, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
+                         nsplit);
       break;
     case 128:
       hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
-                         part, H, max_ctx, window, (int)long_layer, scale, shift, eps, nsplit);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
-hipError_t attn_decode_combine(const float* part, bf16_t* out, int B, int H, int Dh, int nsplit,
-                               hipStream_t st) {
-  switch (Dh) {
-    case 64:
-      hipLaunchKernelGGL(k_attn_dec_combine<64>, dim3(H, B), dim3(64), 0, st, part, out, H, nsplit);
-      break;
-    case 128:
-      hipLaunchKernelGGL(k_attn_dec_combine<128>, dim3(H, B), dim3(128), 0, st, part, out, H, nsplit);
+                         part, cnt, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
+                         nsplit);
       break;
     default:
       return hipErrorInvalidValue;

@@ -74,7 +74,7 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, skcnt, skpart, x, x0, qkv, q, ao, hn, hid, rs, part, zb, total;
+  size_t pos, sp, steps, amax, skcnt, skpart, acnt, x, x0, qkv, q, ao, hn, hid, rs, part, zb, total;
 };
 constexpr int SK_MAX_TILES = 4096;          // split-K counters of the skinny GEMM
 constexpr size_t SK_PART_FLOATS = 512 * 1024;  // split-K partial tiles (<= 512 of 1024)
@@ -89,6 +89,7 @@ SLayout ws_layout(const ann_config& c) {
   s.amax = off; off += up((B <= 8 ? B : 1) * (size_t)gemv_blocks(c.V, c.d) * 8);
   s.skcnt = off; off += up(SK_MAX_TILES * 4);
   s.skpart = off; off += up(SK_PART_FLOATS * 4);
+  s.acnt = off; off += up(B * c.H * 4);
   s.x = off; off += up(M * d * 2);
   s.x0 = off; off += up(M * d * 2);
   s.qkv = off; off += up(M * 3 * d * 2);
@@ -202,13 +203,12 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
 
 // y = pre(X) @ W^T for M rows with the given epilogue.
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
-         int M, int N, int K, EpiArgs ea, hipStream_t st, PreArgs pa = PreArgs{}) {
+         int M, int N, int K, EpiArgs ea, hipStream_t st) {
   const bool use_gemv = gemv_fits(M, K);
   // the skinny GEMM re-reads A per 16 columns: wide outputs (lm_head) go to
   // the large-tile GEMM
   const bool use_sk = !use_gemv && M <= 64 && N <= 8 * K &&
                       (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <= SK_PART_FLOATS;
-  if (pre == PRE_ATTN && !use_gemv) return fail(ANN_E_ARG, "attention prologue needs the GEMV");
   float* rs = nullptr;
   if (pre == PRE_RMS && use_sk) {   // row scales applied as the skinny GEMM loads A
     rs = c->sp<float>(c->sl.rs);
@@ -222,7 +222,7 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   }
   ProfScope ps(c, kind, st);
   if (use_gemv)
-    HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, pa, st));
+    HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, st));
   else if (use_sk)
     HIPCHK(gemm_skinny(epi, rs, X, ldx, W, M, N, K, ea, c->sp<float>(c->sl.skpart),
                        c->sp<unsigned>(c->sl.skcnt), st));
@@ -231,12 +231,17 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   return ANN_OK;
 }
 
-// Fixed split counts of the decode attention (independent of the current
-// length, so a captured step replays for every position).
-int dec_splits(const ann_config& g, bool lng) {
+// Split count of the decode attention: enough work-groups (about 1024) to
+// fill the GPU, at most one 64-key chunk per split of the longest key range.
+// Independent of the current length, so a captured step replays at every
+// position.
+int dec_splits(const ann_config& g, bool lng, int B) {
   const int keys = lng ? g.max_ctx : (g.window < g.max_ctx ? g.window : g.max_ctx);
   int n = (keys + 63) / 64;
-  return n < 1 ? 1 : (n > MAX_SPLIT ? MAX_SPLIT : n);
+  if (n > MAX_SPLIT) n = MAX_SPLIT;
+  const int want = (1024 + B * g.H - 1) / (B * g.H);
+  if (n > want) n = want;
+  return n < 1 ? 1 : n;
 }
 
 // embed + all layers for M = B*T rows whose positions start at pos[b].
@@ -269,22 +274,16 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
     er.x0 = x0;
     er.ldr = d;
     er.lam = lam + 8 * l;
-    if (T == 1) {  // decode: fused QK-norm / RoPE / KV append, split partials
-      const int ns = dec_splits(g, lng);
+    if (T == 1) {  // decode: fused QK-norm / RoPE / KV append and split combine
+      const int ns = dec_splits(g, lng, B);
       {
         ProfScope ps(c, ANN_PROF_ATTN, st);
-        HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part, B, H, Dh,
-                           g.max_ctx, g.window, lng, g.attn_scale, g.rms_eps, ns, st));
+        HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part,
+                           c->sp<unsigned>(c->sl.acnt), ao, B, H, Dh, g.max_ctx, g.window, lng,
+                           g.attn_scale, g.rms_eps, ns, st));
       }
-      if (gemv_fits(M, d) && H <= 16) {
-        PreArgs pa{part, H, Dh, ns};
-        rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_ATTN, c->layer_w(l, c->wl.o), nullptr, d, M,
-                  d, d, er, st, pa);
-      } else {
-        HIPCHK(attn_decode_combine(part, ao, B, H, Dh, ns, st));
-        rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d,
-                  d, er, st);
-      }
+      rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d, d,
+                er, st);
       if (rc) return rc;
     } else {
       HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,

@@ -40,14 +40,8 @@ struct SampParams {
   unsigned long long seed;
 };
 
-// Input prologue of the GEMV: X rows as given, RMS-normalised, or the
-// attention output rebuilt from decode-attention split partials.
-enum { PRE_PLAIN = 0, PRE_RMS = 1, PRE_ATTN = 2 };
-
-struct PreArgs {
-  const float* part;  // (M, H, nsplit, Dh + 1): O (Dh) then L
-  int H, Dh, nsplit;
-};
+// Input prologue of a projection: X rows as given or RMS-normalised.
+enum { PRE_PLAIN = 0, PRE_RMS = 1 };
 
 hipError_t pack_transpose(const float* src, bf16_t* dst, int K, int N, int ldd,
                           const float* scale, hipStream_t st);
@@ -66,7 +60,7 @@ hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const 
 
 // GEMV for M <= 8 rows: y = pre(X) @ W^T, X (M, ldx) bf16.
 hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int M, int N, int K,
-                float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st);
+                float eps, const EpiArgs& ea, hipStream_t st);
 bool gemv_fits(int M, int K);
 int gemv_blocks(int N, int K);
 hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
@@ -99,13 +93,12 @@ hipError_t attn_prefill(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, con
                         bool long_layer, float scale, hipStream_t st);
 
 // Decode attention with fused QK-norm / RoPE / KV append (one token per
-// sequence); writes split partials (B, H, nsplit, Dh + 1).
+// sequence) -> out (B, H*Dh) bf16.  part: split scratch (B, H, nsplit, Dh + 1);
+// cnt: B*H arrival counters, zero between calls.
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
-                       const float* cs, const float* sn, float* part, int B, int H, int Dh,
-                       int max_ctx, int window, bool long_layer, float scale, float eps,
-                       int nsplit, hipStream_t st);
-hipError_t attn_decode_combine(const float* part, bf16_t* out, int B, int H, int Dh, int nsplit,
-                               hipStream_t st);
+                       const float* cs, const float* sn, float* part, unsigned* cnt, bf16_t* out,
+                       int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
+                       float eps, int nsplit, hipStream_t st);
 
 // Sampling of B rows of bf16 z (B, ldz) over the first Vs entries with the
 // device-resident parameters; uses and increments steps[b]; advances pos[b]

@@ -52,33 +52,9 @@ __device__ __forceinline__ uint32_t zkey(bf16_t h) {  // order-preserving 16-bit
 // Fill the LDS activation tile xs (M x K bf16) per the prologue PRE.
 template <int M, int PRE>
 __device__ __forceinline__ void gemv_prologue(uint4* xs4, const bf16_t* __restrict__ X, int ldx,
-                                              int K, float eps, const PreArgs& pa, float* red) {
+                                              int K, float eps, float* red) {
   const int tid = threadIdx.x;
   const int K8 = K >> 3;
-  if (PRE == PRE_ATTN) {
-    // o[m][h*Dh + e] = sum_s O_s / sum_s L_s, rounded once to bf16; nsplit
-    // <= 32, every split's O and L loads issued before any is consumed
-    const int Dh = pa.Dh, ns = pa.nsplit, st = Dh + 1, H = pa.H;
-    bf16_t* xs = (bf16_t*)xs4;
-    for (int i = tid; i < M * K; i += GEMV_THREADS) {
-      const int m = i / K, k = i % K, h = k / Dh, e = k % Dh;
-      const float* pp = pa.part + ((size_t)m * H + h) * ns * st;
-      float v[32], l[32];
-#pragma unroll
-      for (int s = 0; s < 32; ++s) {
-        v[s] = s < ns ? pp[s * st + e] : 0.f;
-        l[s] = s < ns ? pp[s * st + Dh] : 0.f;
-      }
-      float o = 0.f, L = 0.f;
-#pragma unroll
-      for (int s = 0; s < 32; ++s) {
-        o += v[s];
-        L += l[s];
-      }
-      xs[i] = f2bf(o / L);
-    }
-    return;
-  }
   float scale[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) scale[m] = 1.f;
@@ -124,11 +100,10 @@ __device__ __forceinline__ void gemv_prologue(uint4* xs4, const bf16_t* __restri
 template <int M, int LPR, int EPI, int PRE, int GEMV_U>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict__ W,
                                                        const bf16_t* __restrict__ X, int ldx,
-                                                       int N, int K, float eps, EpiArgs ea,
-                                                       PreArgs pa) {
+                                                       int N, int K, float eps, EpiArgs ea) {
   extern __shared__ uint4 xs4[];                 // M * K bf16 activations
   constexpr int G = GEMV_THREADS / LPR;          // weight rows per work-group
-  __shared__ float red[M * 16 > 128 ? M * 16 : 128];
+  __shared__ float red[M * (GEMV_THREADS / 64)];
   __shared__ unsigned long long s_key[G][M];
   const int tid = threadIdx.x;
   const int K8 = K >> 3;
@@ -149,7 +124,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const bf16_t* __restrict_
     const int c = u * LPR + lig;
     w[u] = (live && c < K8) ? wrow[c] : make_uint4(0, 0, 0, 0);
   }
-  gemv_prologue<M, PRE>(xs4, X, ldx, K, eps, pa, red);
+  gemv_prologue<M, PRE>(xs4, X, ldx, K, eps, red);
   __syncthreads();
 
   for (int c0 = 0; c0 < K8; c0 += LPR * GEMV_U) {
@@ -260,34 +235,33 @@ bool gemv_fits(int M, int K) {
 // whole row slice when K / (8 LPR) <= 8, without spilling for short rows.
 template <int M, int LPR, int EPI, int PRE>
 static hipError_t launch_gemv(const bf16_t* W, const bf16_t* X, int ldx, int N, int K, float eps,
-                              const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
+                              const EpiArgs& ea, hipStream_t st) {
   constexpr int G = GEMV_THREADS / LPR;
   dim3 grid((N + G - 1) / G);
   size_t lds = (size_t)M * K * 2;
   if ((K >> 3) <= 4 * LPR)
     hipLaunchKernelGGL((k_gemv<M, LPR, EPI, PRE, 4>), grid, dim3(GEMV_THREADS), lds, st, W, X,
-                       ldx, N, K, eps, ea, pa);
+                       ldx, N, K, eps, ea);
   else
     hipLaunchKernelGGL((k_gemv<M, LPR, EPI, PRE, 8>), grid, dim3(GEMV_THREADS), lds, st, W, X,
-                       ldx, N, K, eps, ea, pa);
+                       ldx, N, K, eps, ea);
   return hipGetLastError();
 }
 
 template <int M, int EPI, int PRE>
 static hipError_t gemv_lpr(const bf16_t* W, const bf16_t* X, int ldx, int N, int K, float eps,
-                           const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
-  if (K <= 1024) return launch_gemv<M, 32, EPI, PRE>(W, X, ldx, N, K, eps, ea, pa, st);
-  return launch_gemv<M, 64, EPI, PRE>(W, X, ldx, N, K, eps, ea, pa, st);
+                           const EpiArgs& ea, hipStream_t st) {
+  if (K <= 1024) return launch_gemv<M, 32, EPI, PRE>(W, X, ldx, N, K, eps, ea, st);
+  return launch_gemv<M, 64, EPI, PRE>(W, X, ldx, N, K, eps, ea, st);
 }
 
 template <int M>
 static hipError_t gemv_m(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int N,
-                         int K, float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
+                         int K, float eps, const EpiArgs& ea, hipStream_t st) {
 #define ANN_GEMV_PRE(E)                                                                 \
   switch (pre) {                                                                        \
-    case PRE_PLAIN: return gemv_lpr<M, E, PRE_PLAIN>(W, X, ldx, N, K, eps, ea, pa, st); \
-    case PRE_RMS: return gemv_lpr<M, E, PRE_RMS>(W, X, ldx, N, K, eps, ea, pa, st);     \
-    case PRE_ATTN: return gemv_lpr<M, E, PRE_ATTN>(W, X, ldx, N, K, eps, ea, pa, st);   \
+    case PRE_PLAIN: return gemv_lpr<M, E, PRE_PLAIN>(W, X, ldx, N, K, eps, ea, st); \
+    case PRE_RMS: return gemv_lpr<M, E, PRE_RMS>(W, X, ldx, N, K, eps, ea, st);     \
   }                                                                                     \
   break;
   switch (epi) {
@@ -302,17 +276,17 @@ static hipError_t gemv_m(int epi, int pre, const bf16_t* W, const bf16_t* X, int
 }
 
 hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int M, int N, int K,
-                float eps, const EpiArgs& ea, const PreArgs& pa, hipStream_t st) {
+                float eps, const EpiArgs& ea, hipStream_t st) {
   if (!gemv_fits(M, K)) return hipErrorInvalidValue;
   switch (M) {
-    case 1: return gemv_m<1>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 2: return gemv_m<2>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 3: return gemv_m<3>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 4: return gemv_m<4>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 5: return gemv_m<5>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 6: return gemv_m<6>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 7: return gemv_m<7>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
-    case 8: return gemv_m<8>(epi, pre, W, X, ldx, N, K, eps, ea, pa, st);
+    case 1: return gemv_m<1>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 2: return gemv_m<2>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 3: return gemv_m<3>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 4: return gemv_m<4>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 5: return gemv_m<5>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 6: return gemv_m<6>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 7: return gemv_m<7>(epi, pre, W, X, ldx, N, K, eps, ea, st);
+    case 8: return gemv_m<8>(epi, pre, W, X, ldx, N, K, eps, ea, st);
   }
   return hipErrorInvalidValue;
 }

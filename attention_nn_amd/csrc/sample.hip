@@ -7,8 +7,8 @@
 //     every zc >= kth (ties included, as `where(z < kth, -1e9, z)`); draw
 //     u ~ U[0,1) from Philox4x32-10 and return the first kept index whose
 //     running sum of exp(zc - max) exceeds u * total.
-// The k-th largest is found by a two-pass radix select on the 16-bit ordered
-// keys of z in LDS histograms; one work-group per row.
+// The k-th largest is found by a binary search over the 16-bit ordered keys
+// of z (count of keys >= T per round); one work-group per row.
 #include <math.h>
 #include "common.h"
 #include "launch.h"
@@ -54,20 +54,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
-// Largest bin b with count(bins >= b) >= need (bins scanned from the top).
-__device__ int select_bin(const uint32_t* hist, uint32_t need, uint32_t* above) {
-  uint32_t acc = 0;
-  for (int bn = 255; bn >= 0; --bn) {
-    if (acc + hist[bn] >= need) {
-      *above = acc;
-      return bn;
-    }
-    acc += hist[bn];
-  }
-  *above = acc;
-  return 0;
-}
-
 constexpr int SMP_CH = 7;  // 16-byte chunks per thread: 1024 * 56 >= 50257
 
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
@@ -94,7 +80,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   const float temperature = sp->temperature;
   const int top_k = sp->top_k;
   const uint64_t seed = sp->seed;
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_cnt[2][SMP_THREADS / 64];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
   __shared__ float s_wsum[SMP_THREADS / 64];
   __shared__ uint32_t s_misc[4];
@@ -130,63 +116,61 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     return;
   }
 
-  // ---- k-th largest 16-bit key (exact) when top-k applies
-  uint32_t thr_key = 0;
-  const bool use_thr = top_k > 0 && top_k < Vs;
-  if (use_thr) {
-    for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < SMP_CH * 8; ++i)
-      if (base + i < Vs) atomicAdd(&hist[okey(elem(i)) >> 8], 1u);
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t above;
-      const int b1 = select_bin(hist, (uint32_t)top_k, &above);
-      s_misc[0] = (uint32_t)b1;
-      s_misc[1] = (uint32_t)top_k - above;
-    }
-    __syncthreads();
-    const uint32_t b1 = s_misc[0];
-    for (int i = tid; i < 256; i += SMP_THREADS) hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < SMP_CH * 8; ++i) {
-      const uint32_t k = okey(elem(i));
-      if (base + i < Vs && (k >> 8) == b1) atomicAdd(&hist[k & 0xffu], 1u);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t above;
-      const int b2 = select_bin(hist, s_misc[1], &above);
-      s_misc[2] = (b1 << 8) | (uint32_t)b2;
-    }
-    __syncthreads();
-    thr_key = s_misc[2];
-  }
-
-  // ---- threshold and maximum in the softcapped / tempered domain
+  // ---- maximum key, then the k-th largest key (exact) when top-k applies:
+  // binary search for the largest T with count(key >= T) >= top_k; each
+  // round counts from registers and reduces once over the work-group
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < SMP_CH * 8; ++i)
     if (base + i < Vs) kmax = max(kmax, okey(elem(i)));
   kmax = (uint32_t)block_max_u64(kmax, s_red);
+  uint32_t thr_key = 0;
+  const bool use_thr = top_k > 0 && top_k < Vs;
+  if (use_thr) {
+    uint32_t lo = 0, hi = kmax;
+    int round = 0;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      uint32_t c = 0;
+#pragma unroll
+      for (int i = 0; i < SMP_CH * 8; ++i) c += (base + i < Vs && okey(elem(i)) >= mid) ? 1u : 0u;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+      uint32_t* cb = s_cnt[round & 1];
+      if (lane == 0) cb[wv] = c;
+      __syncthreads();
+      uint32_t tot = 0;
+#pragma unroll
+      for (int w = 0; w < SMP_THREADS / 64; ++w) tot += cb[w];
+      if (tot >= (uint32_t)top_k) lo = mid;
+      else hi = mid - 1;
+      ++round;
+    }
+    thr_key = lo;
+  }
+  // ---- threshold and maximum in the softcapped / tempered domain
   auto key2bf = [](uint32_t k) -> bf16_t {
     return (bf16_t)((k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu));
   };
   const float tmp = temperature;
   const float zmax = softcap(bf2f(key2bf(kmax))) / tmp;
   const float zthr = use_thr ? softcap(bf2f(key2bf(thr_key))) / tmp : -INFINITY;
+  // softcap / temperature is non-decreasing in z, so "kept" (zc >= zthr) is
+  // "key >= thr_key" unless the value just below the threshold rounds to the
+  // same zc (saturated softcap): checked once, exact fallback otherwise.
+  const bool by_key = !use_thr || thr_key == 0 ||
+                      softcap(bf2f(key2bf(thr_key - 1))) / tmp < zthr;
+  auto kept = [&](int i) -> bool {
+    if (base + i >= Vs) return false;
+    const bf16_t h = elem(i);
+    return by_key ? okey(h) >= thr_key : softcap(bf2f(h)) / tmp >= zthr;
+  };
 
   // ---- weights of this thread's slice, block exclusive scan (fixed order)
   float local = 0.f;
 #pragma unroll
-  for (int i = 0; i < SMP_CH * 8; ++i) {
-    if (base + i < Vs) {
-      const float zc = softcap(bf2f(elem(i))) / tmp;
-      if (zc >= zthr) local += expf(zc - zmax);
-    }
-  }
+  for (int i = 0; i < SMP_CH * 8; ++i)
+    if (kept(i)) local += expf(softcap(bf2f(elem(i))) / tmp - zmax);
   float incl = local;   // inclusive scan within the wave
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -212,13 +196,10 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     int pick = -1, last = -1;
 #pragma unroll
     for (int i = 0; i < SMP_CH * 8; ++i) {
-      if (pick < 0 && base + i < Vs) {
-        const float zc = softcap(bf2f(elem(i))) / tmp;
-        if (zc >= zthr) {
-          last = base + i;
-          run += expf(zc - zmax);
-          if (target < run) pick = base + i;
-        }
+      if (pick < 0 && kept(i)) {
+        last = base + i;
+        run += expf(softcap(bf2f(elem(i))) / tmp - zmax);
+        if (target < run) pick = base + i;
       }
     }
     if (pick < 0) pick = last;
@@ -230,7 +211,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     int lastk = -1;
 #pragma unroll
     for (int i = 0; i < SMP_CH * 8; ++i)
-      if (base + i < Vs && softcap(bf2f(elem(i))) / tmp >= zthr) lastk = base + i;
+      if (kept(i)) lastk = base + i;
     __syncthreads();
     if (tid == 0) s_misc[2] = 0;
     __syncthreads();
