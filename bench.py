@@ -75,6 +75,19 @@ def lm_head_bytes(cfg, B):
     return 2 * d * V + 2 * B * d + 2 * B * V
 
 
+def lm_head_traffic():
+    """HBM bytes per lm_head launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (scaled by a known-size copy), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "lm_head_b1_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return int((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=True):
     import torch
     B = prompt.shape[0]
@@ -244,7 +257,9 @@ def main():
                                "to context 1024", "global_batch": 1, "seq_len": 1024,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": lm_head_traffic(),
+                     "traffic_source": "profiles/lm_head_b1_hbm_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
                      "kernel": "k_gemv<1,32,EPI_LOGITS,rms> (lm_head + softcap)",
                      "bytes_per_launch": head_b, "avg_launch_us": round(head_avg_ms * 1e3, 3),
                      "launches": head_n},
