@@ -190,6 +190,43 @@ def secondary_b64(cfg, params):
     }
 
 
+def extra_config(name):
+    """prefill then decode, reported as secondary lines."""
+    import torch
+    from attention_nn_amd.config import cfg_155m, cfg_834m
+    from attention_nn_amd.engine import Engine
+    from attention_nn_amd.weights import init_params
+    if name == "cfg4":
+        cfg, B, P, S = cfg_155m(seq_len=8192), 16, 7680, 512
+        desc = "cfg4: 155M, B=16, 7680-token prompts + 512 decode steps (ctx 8192), greedy"
+        temp, k = 0.0, 0
+    else:
+        cfg, B, P, S = cfg_834m(seq_len=2048), 128, 1024, 1024
+        desc = "cfg5: d1536 L24 H12x128, B=128, 1024-token prompts + 1024 steps, softcap + top-k 50"
+        temp, k = 0.8, 50
+    params = init_params(cfg, seed=0, dense=True)
+    eng = Engine(cfg, params, max_batch=B, max_ctx=P + S, max_tokens=B * P)
+    pr = np.random.default_rng(3).integers(0, 50257, (B, P))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    nxt, _ = eng.prefill(pr, temp, k, 11, 0)
+    e1.record()
+    torch.cuda.synchronize()
+    pms = e0.elapsed_time(e1)
+    ms, _, _, toks = run_decode(eng, pr, S, 0, temp, k, 11, prof=False)
+    byts = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
+    gbs = byts / (ms / S / 1e3) / 1e9
+    pf = prefill_flops(cfg, B, P)
+    del eng
+    torch.cuda.empty_cache()
+    return {"workload": desc,
+            "decode_tok_s": round(toks / (ms / 1e3), 1), "decode_ms_per_step": round(ms / S, 4),
+            "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "prefill_ms": round(pms, 2), "prefill_tflops": round(pf / (pms / 1e3) / 1e12, 2),
+            "prefill_mfma_frac": round(pf / (pms / 1e3) / 1e12 / MFMA_BF16_TFLOPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +236,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-b64", action="store_true",
                     help="run only the batch-64 prefill/decode section (for profiling)")
+    ap.add_argument("--configs", type=str, default="",
+                    help="comma list of extra workloads to add as secondary lines: cfg4,cfg5")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 512 MiB device-to-device (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -273,6 +312,8 @@ def main():
 
     if not args.no_secondary:
         sec.update(secondary_b64(cfg, params))
+    for name in [c for c in args.configs.split(",") if c]:
+        sec[name] = extra_config(name)
     out["secondary"] = sec
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, params, prompt_len, 1024)

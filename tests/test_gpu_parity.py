@@ -139,6 +139,27 @@ def test_decode_teacher_forced_past_window(name, B):
     assert worst < LOGIT_TOL, worst
 
 
+def test_long_context_decode():
+    """Decode at positions up to 2100 on a full-causal layer (the split count
+    caps at 32, several 64-key chunks per split) and a windowed layer."""
+    cfg = GPTConfig(vocab_size=600, num_layers=2, num_heads=2, model_dim=256, seq_len=2112,
+                    window=384, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 31, dense=True))
+    tok = np.random.default_rng(32).integers(0, cfg.vocab_size, (1, 2100))
+    eng = _engine(cfg, p, 1)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :2090], want_logits=True)
+    ref = R.forward(prep, tok[:, :2090], cache)[:, -1]
+    worst = (lg.cpu() - ref).abs().max().item()
+    for i in range(2090, 2099):
+        t = tok[:, i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    assert worst < LOGIT_TOL, worst
+
+
 def test_batch_rows_independent():
     cfg = small_cfgs()["dh128"]
     p = perturb_lambdas(init_params(cfg, 2, dense=True))
