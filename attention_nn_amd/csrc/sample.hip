@@ -7,8 +7,13 @@
 //     every zc >= kth (ties included, as `where(z < kth, -1e9, z)`); draw
 //     u ~ U[0,1) from Philox4x32-10 and return the first kept index whose
 //     running sum of exp(zc - max) exceeds u * total.
-// The k-th largest is found by a binary search over the 16-bit ordered keys
-// of z (count of keys >= T per round); one work-group per row.
+// One work-group of 1024 threads per row; thread t holds the ordered 16-bit
+// keys of entries [56 t, 56 t + 56) in registers, two per dword.  The k-th
+// largest key comes from a binary search (count of keys >= T per round over
+// the packed keys, saturating 16-bit arithmetic) on [lb, kmax], where lb, the
+// k-th largest of the per-thread maxima, bounds it from below (k <= 1024).
+// The weights use the hardware exp2 / reciprocal; only chunks holding a kept
+// entry in some lane of the wave evaluate them.
 #include <math.h>
 #include "common.h"
 #include "launch.h"
@@ -16,9 +21,36 @@
 namespace ann {
 
 constexpr int SMP_THREADS = 1024;
+constexpr int SMP_CH = 7;              // 16-byte chunks (8 entries) per thread
+constexpr int SMP_PER = SMP_CH * 8;    // entries per thread: Vs <= 57344
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t okey(bf16_t h) {  // order-preserving 16-bit key
-  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
+// Two bf16 values of a dword -> their order-preserving 16-bit keys
+// (negative: ~h, non-negative: h | 0x8000).
+__device__ __forceinline__ uint32_t okey2(uint32_t w) {
+  return w ^ (0x80008000u | (((w >> 15) & 0x00010001u) * 0x7fffu));
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+  const uint32_t h = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+  return __uint_as_float(h << 16);
+}
+// Softcap with the hardware exp2 and reciprocal (weights only; the threshold
+// comparisons use the IEEE softcap).
+__device__ __forceinline__ float softcap_fast(float z) {
+  const float e = __builtin_amdgcn_exp2f((z + 5.0f) * -0.19235933878519512f);  // -log2(e) / 7.5
+  return 23.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
+// Number of packed 16-bit keys >= t (t >= 1): sat(key - (t - 1)) > 0.
+__device__ __forceinline__ uint32_t count_ge(const uint32_t* kk, uint32_t t) {
+  const unsigned short t1 = (unsigned short)(t - 1);
+  const u16x2 tm = {t1, t1}, one = {1, 1};
+  u16x2 acc = {0, 0};
+#pragma unroll
+  for (int j = 0; j < SMP_PER / 2; ++j) {
+    const u16x2 v = __builtin_bit_cast(u16x2, kk[j]);
+    acc += __builtin_elementwise_min(__builtin_elementwise_sub_sat(v, tm), one);
+  }
+  return (uint32_t)acc.x + (uint32_t)acc.y;
 }
 
 __device__ __forceinline__ uint32_t mulhilo(uint32_t a, uint32_t b, uint32_t* hi) {
@@ -54,8 +86,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
-constexpr int SMP_CH = 7;  // 16-byte chunks per thread: 1024 * 56 >= 50257
-
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   v = wave_max_u64(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -68,46 +98,65 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   return b;
 }
 
-// One work-group per row; thread t holds the contiguous slice
-// [56 t, 56 t + 56) of the row in registers, so the row is read from memory
-// once and every pass (radix select, max, weights, scan, draw) runs on
-// registers and LDS.
+// Block sum of per-thread counts; buf alternates between calls so that one
+// barrier per call suffices.
+__device__ __forceinline__ uint32_t block_count(uint32_t c, uint32_t* buf) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = c;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) t += buf[w];
+  return t;
+}
+
 __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
                                                         int Vs, const SampParams* __restrict__ sp,
                                                         unsigned long long* __restrict__ steps,
                                                         int32_t* __restrict__ out_tok,
                                                         int32_t* __restrict__ pos, int pos_adv) {
-  const float temperature = sp->temperature;
-  const int top_k = sp->top_k;
-  const uint64_t seed = sp->seed;
   __shared__ uint32_t s_cnt[2][SMP_THREADS / 64];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
   __shared__ float s_wsum[SMP_THREADS / 64];
-  __shared__ uint32_t s_misc[4];
+  __shared__ uint32_t s_misc[2];
+  const float temperature = sp->temperature;
+  const int top_k = sp->top_k;
+  const uint64_t seed = sp->seed;
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const bf16_t* z = zall + (size_t)row * ldz;
-  const int base = tid * SMP_CH * 8;
+  const int base = tid * SMP_PER;
+  const int nvalid = max(0, min(SMP_PER, Vs - base));
 
-  uint4 raw[SMP_CH];
+  // ---- keys of this thread's entries; entries >= Vs get key 0.  A chunk
+  // that starts below Vs lies inside the row's padded width (ldz >= Vs
+  // rounded up to 8, checked on the host).
+  uint32_t kk[SMP_PER / 2];
 #pragma unroll
-  for (int c = 0; c < SMP_CH; ++c)
-    raw[c] = (base + c * 8 < ldz) ? *(const uint4*)(z + base + c * 8) : make_uint4(0, 0, 0, 0);
-  auto elem = [&](int i) -> bf16_t {   // i in [0, 56)
-    const uint4& w = raw[i >> 3];
-    const uint32_t word = (i & 7) < 2 ? w.x : (i & 7) < 4 ? w.y : (i & 7) < 6 ? w.z : w.w;
-    return (bf16_t)((i & 1) ? (word >> 16) : (word & 0xffffu));
-  };
+  for (int c = 0; c < SMP_CH; ++c) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (c * 8 < nvalid) v = *(const uint4*)(z + base + c * 8);
+    kk[4 * c + 0] = okey2(v.x);
+    kk[4 * c + 1] = okey2(v.y);
+    kk[4 * c + 2] = okey2(v.z);
+    kk[4 * c + 3] = okey2(v.w);
+  }
+  if (nvalid < SMP_PER) {
+#pragma unroll
+    for (int j = 0; j < SMP_PER / 2; ++j)
+      kk[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
+  }
+  uint32_t lmax = 0;
+  int lidx = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_PER / 2; ++j) {
+    const uint32_t lo = kk[j] & 0xffffu, hi = kk[j] >> 16;
+    if (lo > lmax) { lmax = lo; lidx = 2 * j; }
+    if (hi > lmax) { lmax = hi; lidx = 2 * j + 1; }
+  }
 
-  if (temperature == 0.f) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < SMP_CH * 8; ++i) {
-      const int gi = base + i;
-      if (gi < Vs) {
-        const uint64_t key = ((uint64_t)okey(elem(i)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)gi);
-        best = key > best ? key : best;
-      }
-    }
+  if (temperature == 0.f) {   // greedy: maximal key, lowest index on ties
+    uint64_t best = ((uint64_t)lmax << 32) | (uint64_t)(0xffffffffu - (uint32_t)(base + lidx));
     best = block_max_u64(best, s_red);
     if (tid == 0) {
       out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
@@ -115,71 +164,92 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     }
     return;
   }
+  const uint32_t kmax = (uint32_t)block_max_u64(lmax, s_red);
 
-  // ---- maximum key, then the k-th largest key (exact) when top-k applies:
-  // binary search for the largest T with count(key >= T) >= top_k; each
-  // round counts from registers and reduces once over the work-group
-  uint32_t kmax = 0;
-#pragma unroll
-  for (int i = 0; i < SMP_CH * 8; ++i)
-    if (base + i < Vs) kmax = max(kmax, okey(elem(i)));
-  kmax = (uint32_t)block_max_u64(kmax, s_red);
+  // ---- k-th largest key: largest T with count(key >= T) >= top_k
   uint32_t thr_key = 0;
   const bool use_thr = top_k > 0 && top_k < Vs;
   if (use_thr) {
     uint32_t lo = 0, hi = kmax;
     int round = 0;
+    if (top_k <= SMP_THREADS) {
+      // lower bound: the top_k-th largest per-thread maximum (top_k threads
+      // each hold a key >= it)
+      uint32_t a = 0, b = kmax;
+      while (a < b) {
+        const uint32_t mid = (a + b + 1) >> 1;
+        const uint32_t c = (uint32_t)__popcll(__ballot(lmax >= mid));
+        const uint32_t tot = block_count(lane == 0 ? c : 0u, s_cnt[round++ & 1]);
+        if (tot >= (uint32_t)top_k) a = mid;
+        else b = mid - 1;
+      }
+      lo = a;
+    }
     while (lo < hi) {
       const uint32_t mid = (lo + hi + 1) >> 1;
-      uint32_t c = 0;
-#pragma unroll
-      for (int i = 0; i < SMP_CH * 8; ++i) c += (base + i < Vs && okey(elem(i)) >= mid) ? 1u : 0u;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-      uint32_t* cb = s_cnt[round & 1];
-      if (lane == 0) cb[wv] = c;
-      __syncthreads();
-      uint32_t tot = 0;
-#pragma unroll
-      for (int w = 0; w < SMP_THREADS / 64; ++w) tot += cb[w];
+      const uint32_t tot = block_count(count_ge(kk, mid), s_cnt[round++ & 1]);
       if (tot >= (uint32_t)top_k) lo = mid;
       else hi = mid - 1;
-      ++round;
     }
     thr_key = lo;
   }
-  // ---- threshold and maximum in the softcapped / tempered domain
-  auto key2bf = [](uint32_t k) -> bf16_t {
-    return (bf16_t)((k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu));
-  };
-  const float tmp = temperature;
-  const float zmax = softcap(bf2f(key2bf(kmax))) / tmp;
-  const float zthr = use_thr ? softcap(bf2f(key2bf(thr_key))) / tmp : -INFINITY;
-  // softcap / temperature is non-decreasing in z, so "kept" (zc >= zthr) is
-  // "key >= thr_key" unless the value just below the threshold rounds to the
-  // same zc (saturated softcap): checked once, exact fallback otherwise.
-  const bool by_key = !use_thr || thr_key == 0 ||
-                      softcap(bf2f(key2bf(thr_key - 1))) / tmp < zthr;
-  auto kept = [&](int i) -> bool {
-    if (base + i >= Vs) return false;
-    const bf16_t h = elem(i);
-    return by_key ? okey(h) >= thr_key : softcap(bf2f(h)) / tmp >= zthr;
-  };
 
-  // ---- weights of this thread's slice, block exclusive scan (fixed order)
+  // ---- kept set = keys >= tk.  softcap / temperature is non-decreasing in
+  // z, so zc >= zc(thr_key) is key >= thr_key unless keys below thr_key
+  // round to the same zc (saturated softcap): then tk is the smallest such
+  // key, found by bisection on the IEEE softcap.
+  const float tmp = temperature;
+  uint32_t tk = thr_key > 1u ? thr_key : 1u;
+  if (use_thr && thr_key > 1u) {
+    const float zthr = softcap(key2f(thr_key)) / tmp;
+    if (softcap(key2f(thr_key - 1)) / tmp >= zthr) {
+      uint32_t a = 1, b = thr_key - 1;   // smallest key in [1, thr_key-1] with f >= zthr
+      while (a < b) {
+        const uint32_t mid = (a + b) >> 1;
+        if (softcap(key2f(mid)) / tmp >= zthr) b = mid;
+        else a = mid + 1;
+      }
+      tk = a;
+    }
+  }
+
+  // ---- weights exp((zc - zc_max) / T) of kept entries, per 8-entry chunk
+  const float c2 = 1.4426950408889634f / tmp;   // log2(e) / T
+  const float scmax = softcap_fast(key2f(kmax));
+  auto wt = [&](uint32_t k) -> float {
+    return __builtin_amdgcn_exp2f((softcap_fast(key2f(k)) - scmax) * c2);
+  };
+  float csum[SMP_CH];
   float local = 0.f;
+  int lastk = -1;
 #pragma unroll
-  for (int i = 0; i < SMP_CH * 8; ++i)
-    if (kept(i)) local += expf(softcap(bf2f(elem(i))) / tmp - zmax);
-  float incl = local;   // inclusive scan within the wave
+  for (int c = 0; c < SMP_CH; ++c) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 4 * c; j < 4 * c + 4; ++j) {
+      const uint32_t lo = kk[j] & 0xffffu, hi = kk[j] >> 16;
+      const bool klo = lo >= tk, khi = hi >= tk;
+      if (__ballot(klo || khi)) {
+        if (klo) { s += wt(lo); lastk = base + 2 * j; }
+        if (khi) { s += wt(hi); lastk = base + 2 * j + 1; }
+      }
+    }
+    csum[c] = s;
+    local += s;
+  }
+
+  // ---- block exclusive scan of the per-thread sums (fixed order)
+  float incl = local;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const float v = __shfl_up(incl, o, 64);
     if (lane >= o) incl += v;
   }
   if (lane == 63) s_wsum[wv] = incl;
+  if (tid == 0) { s_misc[0] = 0xffffffffu; s_misc[1] = 0u; }
   __syncthreads();
   float wbase = 0.f, total = 0.f;
+#pragma unroll
   for (int w = 0; w < SMP_THREADS / 64; ++w) {
     if (w < wv) wbase += s_wsum[w];
     total += s_wsum[w];
@@ -189,38 +259,33 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   const uint32_t rw = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
                                (uint32_t)seed, (uint32_t)(seed >> 32));
   const float target = (float)(rw >> 8) * (1.0f / 16777216.0f) * total;
-  if (tid == 0) s_misc[0] = 0xffffffffu;
-  __syncthreads();
+
+  // ---- the thread whose interval holds the target walks its entries
   if (local > 0.f && target >= before && target < before + local) {
     float run = before;
-    int pick = -1, last = -1;
+    int pick = -1;
 #pragma unroll
-    for (int i = 0; i < SMP_CH * 8; ++i) {
-      if (pick < 0 && kept(i)) {
-        last = base + i;
-        run += expf(softcap(bf2f(elem(i))) / tmp - zmax);
-        if (target < run) pick = base + i;
+    for (int c = 0; c < SMP_CH; ++c) {
+      if (pick < 0 && target < run + csum[c]) {
+        float s = 0.f;   // same additions as csum[c]: reaches run + csum[c]
+#pragma unroll
+        for (int j = 4 * c; j < 4 * c + 4; ++j) {
+          const uint32_t lo = kk[j] & 0xffffu, hi = kk[j] >> 16;
+          if (lo >= tk) { s += wt(lo); if (pick < 0 && target < run + s) pick = base + 2 * j; }
+          if (hi >= tk) { s += wt(hi); if (pick < 0 && target < run + s) pick = base + 2 * j + 1; }
+        }
       }
+      run += csum[c];
     }
-    if (pick < 0) pick = last;
+    if (pick < 0) pick = lastk;
     atomicMin(&s_misc[0], (uint32_t)pick);
   }
+  if (lastk >= 0) atomicMax(&s_misc[1], (uint32_t)lastk);
   __syncthreads();
-  if (s_misc[0] == 0xffffffffu) {
-    // rounding put the target at/after the total: take the last kept index
-    int lastk = -1;
-#pragma unroll
-    for (int i = 0; i < SMP_CH * 8; ++i)
-      if (kept(i)) lastk = base + i;
-    __syncthreads();
-    if (tid == 0) s_misc[2] = 0;
-    __syncthreads();
-    if (lastk >= 0) atomicMax(&s_misc[2], (uint32_t)lastk);
-    __syncthreads();
-    if (tid == 0) s_misc[0] = s_misc[2];
-  }
   if (tid == 0) {
-    out_tok[row] = (int32_t)s_misc[0];
+    // rounding can leave the target at/after every interval: last kept entry
+    const uint32_t pick = s_misc[0] != 0xffffffffu ? s_misc[0] : s_misc[1];
+    out_tok[row] = (int32_t)pick;
     if (pos) pos[row] += pos_adv;
     steps[row] = step + 1;
   }
@@ -250,6 +315,8 @@ __global__ void k_advance_pos(int32_t* pos, int B, int n) {
 hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
                   unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
                   hipStream_t st) {
+  if (Vs < 1 || Vs > SMP_THREADS * SMP_PER || ldz % 8 || ((Vs + 7) & ~7) > ldz)
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_sample, dim3(B), dim3(SMP_THREADS), 0, st, z, ldz, Vs, sp, steps, out_tok,
                      pos, pos_adv);
   return hipGetLastError();
