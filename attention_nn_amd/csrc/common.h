@@ -12,12 +12,13 @@ __device__ __forceinline__ float bf2f(bf16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, round to nearest even (gfx950 v_cvt_pk_bf16_f32; equal to
+// the bit-level RNE u + 0x7fff + lsb for every non-NaN input, denormals
+// included); NaN stays a quiet NaN.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float floatx2_hw __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // Round an fp32 value to the nearest bf16 and widen it back.
@@ -31,7 +32,8 @@ __device__ __forceinline__ void unpack8(const uint4& w, float* o) {
 }
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  const floatx2_hw v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw));
 }
 
 template <int W>

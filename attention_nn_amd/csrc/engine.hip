@@ -74,10 +74,8 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, skcnt, skpart, acnt, x, x0, qkv, q, ao, hn, hid, rs, part, zb, total;
+  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, total;
 };
-constexpr int SK_MAX_TILES = 4096;          // split-K counters of the skinny GEMM
-constexpr size_t SK_PART_FLOATS = 512 * 1024;  // split-K partial tiles (<= 512 of 1024)
 
 SLayout ws_layout(const ann_config& c) {
   const size_t d = c.d, M = c.max_tokens, B = c.max_batch, Dh = d / c.H;
@@ -87,8 +85,6 @@ SLayout ws_layout(const ann_config& c) {
   s.sp = off; off += up(sizeof(SampParams));
   s.steps = off; off += up(B * 8);
   s.amax = off; off += up((B <= 8 ? B : 1) * (size_t)gemv_blocks(c.V, c.d) * 8);
-  s.skcnt = off; off += up(SK_MAX_TILES * 4);
-  s.skpart = off; off += up(SK_PART_FLOATS * 4);
   s.acnt = off; off += up(B * c.H * 4);
   s.x = off; off += up(M * d * 2);
   s.x0 = off; off += up(M * d * 2);
@@ -97,7 +93,6 @@ SLayout ws_layout(const ann_config& c) {
   s.ao = off; off += up(M * d * 2);
   s.hn = off; off += up(M * d * 2);
   s.hid = off; off += up(M * 4 * d * 2);
-  s.rs = off; off += up(M * 4);
   s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
   s.zb = off; off += up(B * (size_t)c.V * 2);
   s.total = off;
@@ -205,15 +200,10 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st) {
   const bool use_gemv = gemv_fits(M, K);
-  // the skinny GEMM re-reads A per 16 columns: wide outputs (lm_head) go to
-  // the large-tile GEMM
-  const bool use_sk = !use_gemv && M <= 64 && N <= 8 * K &&
-                      (size_t)((N + 15) / 16) * gemm_sk_split(M, N, K) * 1024 <= SK_PART_FLOATS;
-  float* rs = nullptr;
-  if (pre == PRE_RMS && use_sk) {   // row scales applied as the skinny GEMM loads A
-    rs = c->sp<float>(c->sl.rs);
-    HIPCHK(row_rms_scale(X, ldx, rs, M, K, c->c.rms_eps, st));
-  } else if (pre == PRE_RMS && !use_gemv) {   // large GEMM: A normalised once into h
+  // the skinny GEMM re-reads W per 16 rows and A per 16 columns: wide
+  // outputs (lm_head) go to the large-tile GEMM
+  const bool use_sk = !use_gemv && N <= 8 * K && gemm_skinny_fits(M, N, K, pre == PRE_RMS);
+  if (pre == PRE_RMS && !use_gemv && !use_sk) {   // large GEMM: A normalised once into h
     if (K > c->c.d) return fail(ANN_E_ARG, "RMS prologue wider than the model dim");
     bf16_t* h = c->sp<bf16_t>(c->sl.hn);
     HIPCHK(rms_apply(X, ldx, h, K, M, K, c->c.rms_eps, st));
@@ -224,8 +214,7 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   if (use_gemv)
     HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, st));
   else if (use_sk)
-    HIPCHK(gemm_skinny(epi, rs, X, ldx, W, M, N, K, ea, c->sp<float>(c->sl.skpart),
-                       c->sp<unsigned>(c->sl.skcnt), st));
+    HIPCHK(gemm_skinny(epi, pre == PRE_RMS, X, ldx, W, M, N, K, c->c.rms_eps, ea, st));
   else
     HIPCHK(gemm(epi, X, ldx, W, M, N, K, ea, st));
   return ANN_OK;

@@ -90,38 +90,6 @@ __global__ void k_embed_rms(const int32_t* __restrict__ tok, const bf16_t* __res
   }
 }
 
-// Row scale s_m = rsqrt(mean(x_m^2) + eps) for the GEMM RMS prologue.  One
-// work-group per row; every 16-byte chunk of the row is loaded up front.
-__global__ __launch_bounds__(256) void k_row_rms_scale(const bf16_t* __restrict__ x, int ldx,
-                                                       float* __restrict__ s, int d, float eps) {
-  __shared__ float red[4];
-  const int m = blockIdx.x, tid = threadIdx.x;
-  const uint4* r = (const uint4*)(x + (size_t)m * ldx);
-  const int K8 = d >> 3;
-  uint4 v[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int c = tid + u * 256;
-    v[u] = c < K8 ? r[c] : make_uint4(0, 0, 0, 0);
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    float f[8];
-    unpack8(v[u], f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
-  }
-  for (int c = tid + 1024; c < K8; c += 256) {   // rows longer than 8192
-    float f[8];
-    unpack8(r[c], f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
-  }
-  const float t = block_sum(ss, red);
-  if (tid == 0) s[m] = rsqrtf(t / (float)d + eps);
-}
-
 // h = bf16(x * rsqrt(mean(x^2) + eps)) (model.py:49 with the bf16 output of
 // an eager op); one work-group per row, every chunk loaded up front.
 __global__ __launch_bounds__(256) void k_rms_apply(const bf16_t* __restrict__ x, int ldx,
@@ -308,12 +276,6 @@ hipError_t rope_tables(float* cs, float* sn, int seq_len, int head_dim, float ba
 hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x0, int M, int d,
                      int V, float eps, hipStream_t st) {
   hipLaunchKernelGGL(k_embed_rms, dim3(M), dim3(256), 0, st, tok, emb, x, x0, d, V, eps);
-  return hipGetLastError();
-}
-
-hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
-                         hipStream_t st) {
-  hipLaunchKernelGGL(k_row_rms_scale, dim3(M), dim3(256), 0, st, x, ldx, s, d, eps);
   return hipGetLastError();
 }
 

@@ -52,8 +52,6 @@ hipError_t rope_tables(float* cs, float* sn, int seq_len, int head_dim, float ba
                        hipStream_t st);
 hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x0, int M, int d,
                      int V, float eps, hipStream_t st);
-hipError_t row_rms_scale(const bf16_t* x, int ldx, float* s, int M, int d, float eps,
-                         hipStream_t st);
 hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const int32_t* pos,
                     const float* cs, const float* sn, int M, int T, int H, int Dh, int max_ctx,
                     float eps, hipStream_t st);
@@ -65,13 +63,11 @@ bool gemv_fits(int M, int K);
 int gemv_blocks(int N, int K);
 hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
                            int32_t* pos, int pos_adv, hipStream_t st);
-// Skinny MFMA GEMM for decode (M small, N moderate): y = (rs_m * A) @ W^T;
-// part / cnt: split-K scratch (tiles * ksplit * 1024 floats, tiles counters,
-// counters zero between calls).
-hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const bf16_t* W, int M,
-                       int N, int K, const EpiArgs& ea, float* part, unsigned* cnt,
-                       hipStream_t st);
-int gemm_sk_split(int M, int N, int K);
+// Skinny MFMA GEMM for decode (M <= 64, K % 128 == 0): y = pre(A) @ W^T,
+// rms: A rows RMS-normalised in the kernel (K <= 3072).
+bool gemm_skinny_fits(int M, int N, int K, bool rms);
+hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
+                       int K, float eps, const EpiArgs& ea, hipStream_t st);
 // MFMA GEMM (prefill): y = A @ W^T with A (M, lda) bf16.
 hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                 const EpiArgs& ea, hipStream_t st);

@@ -383,58 +383,62 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
     }
 }
 
-// ---- skinny MFMA GEMM (decode with M <= 64 rows per tile) --------------------
+// ---- skinny MFMA GEMM (decode, M <= 64) -------------------------------------
 //
-// Work-group tile 64 (M) x 16 (N), one 16x16 block per wave; operand fragments
-// go straight from global memory to registers (A rows are L2-resident and
-// shared by every work-group, each weight row is read once), eight k-steps
-// of 32 in flight per lane.  RMS: A rows are scaled by rs[m] and rounded to
-// bf16 as they are loaded.  ksplit > 1 splits K over blockIdx.z; each split writes its
-// partial tile with coherent (sc1) stores and the last split to arrive sums
-// them in split order (deterministic) and runs the epilogue.
+// One 16 (M) x 16 (N) output tile per work-group; the four waves split K into
+// quarters and each loads its whole quarter of A and W fragments (up to 24
+// k-steps of 32) straight into registers before the first MFMA, so a launch
+// waits on memory about once.  The partial tiles are summed through LDS in
+// wave order (deterministic).  RMS: the rows of A are normalised in the
+// kernel -- per-wave sums of squares over the quarter, exchanged through LDS,
+// scale = rsqrt(mean + eps), x * scale rounded to bf16 before the MFMA
+// (model.py:48-49 with the bf16 output of an eager op); needs K <= 3072.
 
-constexpr int SK_D = 8;
+constexpr int SK_KB = 24;
 
 template <int EPI, bool RMS>
 __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, int lda,
-                                                 const float* __restrict__ rs,
                                                  const bf16_t* __restrict__ W, int M, int N, int K,
-                                                 int ksplit, EpiArgs ea,
-                                                 float* __restrict__ part,
-                                                 unsigned* __restrict__ cnt) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 64 + wv * 16, sidx = blockIdx.z;
-  const int kper = K / ksplit, kb = sidx * kper;
+                                                 float eps, EpiArgs ea) {
+  __shared__ floatx4_t red[3 * 64];
+  __shared__ float s_ss[4][16];
+  const int tid = threadIdx.x, lane = tid & 63, wk = tid >> 6;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int kw = K >> 7;   // k-steps per wave
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
   const int arow = m0 + r16, wrow = n0 + r16;
   const bool aok = arow < M, wok = wrow < N;
-  const bf16_t* ap = A + (size_t)(aok ? arow : 0) * lda + kb + kq;
-  const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + kb + kq;
-  const int nsteps = kper >> 5;
-
-  const float scale = (RMS && aok) ? rs[arow] : 1.f;
-
+  const bf16_t* ap = A + (size_t)(aok ? arow : 0) * lda + wk * kw * 32 + kq;
+  const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + wk * kw * 32 + kq;
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-  uint4 ca[SK_D], cw[SK_D], na[SK_D], nw[SK_D];
+  for (int s0 = 0; s0 < kw; s0 += SK_KB) {
+    uint4 ca[SK_KB], cw[SK_KB];
 #pragma unroll
-  for (int i = 0; i < SK_D; ++i) {
-    const bool ok = i < nsteps;
-    ca[i] = (ok && aok) ? *(const uint4*)(ap + i * 32) : make_uint4(0, 0, 0, 0);
-    cw[i] = (ok && wok) ? *(const uint4*)(wp + i * 32) : make_uint4(0, 0, 0, 0);
-  }
-  for (int s0 = 0; s0 < nsteps; s0 += SK_D) {
-    const bool more = s0 + SK_D < nsteps;
-    if (more) {
+    for (int i = 0; i < SK_KB; ++i) {
+      const bool ok = s0 + i < kw;
+      ca[i] = (ok && aok) ? *(const uint4*)(ap + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
+      cw[i] = (ok && wok) ? *(const uint4*)(wp + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
+    }
+    float scale = 1.f;
+    if (RMS) {   // the host guarantees kw <= SK_KB: one pass, uniform barrier
+      float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < SK_D; ++i) {
-        const bool ok = s0 + SK_D + i < nsteps;
-        na[i] = (ok && aok) ? *(const uint4*)(ap + (s0 + SK_D + i) * 32) : make_uint4(0, 0, 0, 0);
-        nw[i] = (ok && wok) ? *(const uint4*)(wp + (s0 + SK_D + i) * 32) : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < SK_KB; ++i) {
+        float f[8];
+        unpack8(ca[i], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
       }
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      if (lane < 16) s_ss[wk][lane] = ss;
+      __syncthreads();
+      const float t = ((s_ss[0][r16] + s_ss[1][r16]) + s_ss[2][r16]) + s_ss[3][r16];
+      scale = rsqrtf(t / (float)K + eps);
     }
 #pragma unroll
-    for (int i = 0; i < SK_D; ++i) {
-      if (s0 + i < nsteps) {
+    for (int i = 0; i < SK_KB; ++i) {
+      if (s0 + i < kw) {
         uint4 a = ca[i];
         if (RMS) {
           float f[8];
@@ -448,76 +452,41 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
                                                       0, 0);
       }
     }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < SK_D; ++i) {
-        ca[i] = na[i];
-        cw[i] = nw[i];
-      }
-    }
   }
-
+  if (wk > 0) red[(wk - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wk > 0) return;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const floatx4_t p = red[j * 64 + lane];
+    acc[0] += p[0];
+    acc[1] += p[1];
+    acc[2] += p[2];
+    acc[3] += p[3];
+  }
   const int n = n0 + r16;
-  if (ksplit == 1) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + (lane >> 4) * 4 + r;
-      if (m < M && n < N) epilogue<EPI>(ea, m, n, acc[r]);
-    }
-    return;
-  }
-  // split-K: coherent partial stores, last arrival reduces in split order
-  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-  float* pt = part + (size_t)tile * ksplit * 1024;
-  const int lr = wv * 16 + (lane >> 4) * 4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __hip_atomic_store(pt + (size_t)sidx * 1024 + (lr + r) * 16 + r16, acc[r], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ unsigned s_last;
-  if (tid == 0) {
-    const unsigned old =
-        __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = old == (unsigned)ksplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float v = 0.f;
-    for (int sp = 0; sp < ksplit; ++sp)
-      v += __hip_atomic_load(pt + (size_t)sp * 1024 + (lr + r) * 16 + r16, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
     const int m = m0 + (lane >> 4) * 4 + r;
-    if (m < M && n < N) epilogue<EPI>(ea, m, n, v);
+    if (m < M && n < N) epilogue<EPI>(ea, m, n, acc[r]);
   }
-  if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-int gemm_sk_split(int M, int N, int K) {
-  // enough work-groups to cover the GPU, each K slice a multiple of 32
-  const int tiles = ((N + 15) / 16) * ((M + 63) / 64);
-  int s = 1;
-  while (tiles * s < 192 && K % (64 * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
-  return s;
+bool gemm_skinny_fits(int M, int N, int K, bool rms) {
+  return M > 0 && M <= 64 && N > 0 && K % 128 == 0 && (!rms || K / 128 <= SK_KB);
 }
 
-hipError_t gemm_skinny(int epi, const float* rs, const bf16_t* A, int lda, const bf16_t* W, int M,
-                       int N, int K, const EpiArgs& ea, float* part, unsigned* cnt,
-                       hipStream_t st) {
-  if (K % 32 || M <= 0) return hipErrorInvalidValue;
-  const bool rms = rs != nullptr;
-  const int ks = gemm_sk_split(M, N, K);
-  dim3 grid((N + 15) / 16, (M + 63) / 64, ks);
+hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
+                       int K, float eps, const EpiArgs& ea, hipStream_t st) {
+  if (!gemm_skinny_fits(M, N, K, rms) || lda % 8) return hipErrorInvalidValue;
+  dim3 grid((N + 15) / 16, (M + 15) / 16);
 #define ANN_SK(E)                                                                            \
   if (rms)                                                                                   \
-    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, rs, W, M, N, K,  \
-                       ks, ea, part, cnt);                                                   \
+    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, W, M, N, K, eps, \
+                       ea);                                                                  \
   else                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, rs, W, M, N, K, \
-                       ks, ea, part, cnt);                                                   \
+    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
+                       eps, ea);                                                             \
   break;
   switch (epi) {
     case EPI_STORE: ANN_SK(EPI_STORE)
