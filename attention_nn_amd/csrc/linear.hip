@@ -394,9 +394,9 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
 // scale = rsqrt(mean + eps), x * scale rounded to bf16 before the MFMA
 // (model.py:48-49 with the bf16 output of an eager op); needs K <= 3072.
 
-constexpr int SK_KB = 24;
+constexpr int SK_KB = 24;   // largest batch of k-steps per wave
 
-template <int EPI, bool RMS>
+template <int EPI, bool RMS, int KB>
 __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, int lda,
                                                  const bf16_t* __restrict__ W, int M, int N, int K,
                                                  float eps, EpiArgs ea) {
@@ -411,19 +411,19 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
   const bf16_t* ap = A + (size_t)(aok ? arow : 0) * lda + wk * kw * 32 + kq;
   const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + wk * kw * 32 + kq;
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < kw; s0 += SK_KB) {
-    uint4 ca[SK_KB], cw[SK_KB];
+  for (int s0 = 0; s0 < kw; s0 += KB) {
+    uint4 ca[KB], cw[KB];
 #pragma unroll
-    for (int i = 0; i < SK_KB; ++i) {
+    for (int i = 0; i < KB; ++i) {
       const bool ok = s0 + i < kw;
       ca[i] = (ok && aok) ? *(const uint4*)(ap + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
       cw[i] = (ok && wok) ? *(const uint4*)(wp + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
     }
     float scale = 1.f;
-    if (RMS) {   // the host guarantees kw <= SK_KB: one pass, uniform barrier
+    if (RMS) {   // the host guarantees kw <= KB: one pass, uniform barrier
       float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < SK_KB; ++i) {
+      for (int i = 0; i < KB; ++i) {
         float f[8];
         unpack8(ca[i], f);
 #pragma unroll
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
       scale = rsqrtf(t / (float)K + eps);
     }
 #pragma unroll
-    for (int i = 0; i < SK_KB; ++i) {
+    for (int i = 0; i < KB; ++i) {
       if (s0 + i < kw) {
         uint4 a = ca[i];
         if (RMS) {
@@ -480,13 +480,26 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
                        int K, float eps, const EpiArgs& ea, hipStream_t st) {
   if (!gemm_skinny_fits(M, N, K, rms) || lda % 8) return hipErrorInvalidValue;
   dim3 grid((N + 15) / 16, (M + 15) / 16);
-#define ANN_SK(E)                                                                            \
-  if (rms)                                                                                   \
-    hipLaunchKernelGGL((k_gemm_sk<E, true>), grid, dim3(256), 0, st, A, lda, W, M, N, K, eps, \
+  // batch depth: the wave's whole K quarter when it fits (fewer registers ->
+  // more resident work-groups)
+  const int kw = K >> 7;
+  const int kb = kw <= 6 ? 6 : kw <= 12 ? 12 : SK_KB;
+#define ANN_SK_KB(E, R)                                                                      \
+  if (kb == 6)                                                                               \
+    hipLaunchKernelGGL((k_gemm_sk<E, R, 6>), grid, dim3(256), 0, st, A, lda, W, M, N, K, eps, \
                        ea);                                                                  \
-  else                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk<E, false>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
+  else if (kb == 12)                                                                         \
+    hipLaunchKernelGGL((k_gemm_sk<E, R, 12>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
                        eps, ea);                                                             \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_gemm_sk<E, R, SK_KB>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
+                       eps, ea);
+#define ANN_SK(E)            \
+  if (rms) {                 \
+    ANN_SK_KB(E, true)       \
+  } else {                   \
+    ANN_SK_KB(E, false)      \
+  }                          \
   break;
   switch (epi) {
     case EPI_STORE: ANN_SK(EPI_STORE)
@@ -496,6 +509,7 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
     case EPI_LOGITS: ANN_SK(EPI_LOGITS)
     default: return hipErrorInvalidValue;
   }
+#undef ANN_SK_KB
 #undef ANN_SK
   return hipGetLastError();
 }
