@@ -19,17 +19,27 @@
 // counter per (b, h) elects that split, which reads them back in split order
 // (deterministic) and resets the counter.
 //
-// Chunk of 64 keys: 4 lanes x 64 B read one 256-B key row (Dh = 128); for
-// P.V 16 lanes x 16 B cover a V row, 16 key groups accumulate in registers
-// and are reduced once through LDS at the end.
+// Each wave walks its own 16-key chunks (chunk t of wave w starts at
+// k0 + 16 (w + 4 t)) with no work-group barrier inside the loop: 4 lanes x
+// Dh/4 dims per key for the scores (bf16 dot2 against the packed q), then
+// Dh/8 lanes x 8 dims per V row for P.V; a ring of three chunks is in flight
+// per wave.  The four waves' (O, L) are summed once through LDS in wave order.
 #include <math.h>
 #include "common.h"
 #include "launch.h"
 
 namespace ann {
 
-constexpr int AD_KC = 64;
 constexpr int AD_THREADS = 256;
+constexpr int AD_KW = 16;    // keys per wave chunk
+constexpr int AD_RING = 3;   // chunks in flight per wave
+
+typedef __bf16 ad_bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ad_bf16x2, a),
+                                         __builtin_bit_cast(ad_bf16x2, b), c, false);
+}
 
 template <int DH>
 __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
@@ -37,21 +47,20 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
     float* __restrict__ part, unsigned* __restrict__ cnt, bf16_t* __restrict__ out, int H,
     int max_ctx, int window, int is_long, float scale, float shift, float eps, int nsplit) {
-  constexpr int TPK = AD_THREADS / AD_KC;   // threads per key in the score pass (4)
-  constexpr int DPT = DH / TPK;             // dims per thread in the score pass
-  constexpr int VL = DH / 8;                // lanes per V row (16-byte slices)
-  constexpr int NG = AD_THREADS / VL;       // key groups in the P.V pass
+  constexpr int KU = DH / 32;       // 16-byte K slices per lane per chunk (4 lanes per key)
+  constexpr int VL = DH / 8;        // lanes per V row
+  constexpr int VP = 64 / VL;       // V rows per pass of the wave
+  constexpr int VU = AD_KW / VP;    // V passes per chunk (== KU)
   constexpr int P = DH / 2, D4 = DH / 4;
 
-  __shared__ float s_q[DH];
-  __shared__ float s_k[DH];
+  __shared__ uint32_t s_qp[P];   // q, k of the new token as bf16 pairs
+  __shared__ uint32_t s_kp[P];
   __shared__ float s_v[DH];
-  __shared__ float s_p[AD_KC];
-  __shared__ float s_o[NG][DH + 1];
+  __shared__ float s_o[AD_THREADS / 64][DH];
   __shared__ float s_l[AD_THREADS / 64];
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int d = H * DH;
   const int p = pos[b];
   const int lo = is_long ? 0 : max(0, p - window + 1);
@@ -59,33 +68,36 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
   const int per = (n + nsplit - 1) / nsplit;
   const int k0 = lo + split * per;
   const int k1 = min(p + 1, k0 + per);
+  const int nch = k1 > k0 ? (k1 - k0 + AD_KW - 1) / AD_KW : 0;
+  const int nt = nch > wv ? (nch - wv + 3) / 4 : 0;   // chunks of this wave
 
   const size_t head_off = ((size_t)b * H + h) * max_ctx;
   const bf16_t* kh = kc + head_off * DH;
   const bf16_t* vh = vc + head_off * DH;
-  const int kk = tid / TPK, qd = (tid % TPK) * DPT;
-  const int vd = (tid % VL) * 8, vg = tid / VL;
-  constexpr int KU = DPT / 8;          // 16-byte K slices per thread per chunk
-  constexpr int VU = AD_KC / NG;       // V rows per thread per chunk
+  const int sk = lane >> 2, sd = (lane & 3) * (DH / 4);   // score: key, first dim
+  const int vr = lane / VL, vd = (lane % VL) * 8;         // P.V: row in pass, dims
 
-  // K/V of a chunk straight into registers (the key at p comes from LDS)
-  auto load_chunk = [&](int c, uint4* kr, uint4* vr) {
-    const int j = c + kk;
+  auto chunk_base = [&](int t) { return k0 + AD_KW * (wv + 4 * t); };
+  auto load = [&](int t, uint4* kr, uint4* vr4) {
+    const int c = chunk_base(t);
+    const int j = c + sk;
     const bool ok = j < k1 && j != p;
 #pragma unroll
     for (int u = 0; u < KU; ++u)
-      kr[u] = ok ? *(const uint4*)(kh + (size_t)j * DH + qd + u * 8) : make_uint4(0, 0, 0, 0);
+      kr[u] = ok ? *(const uint4*)(kh + (size_t)j * DH + sd + u * 8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
-      const int jj = c + vg + u * NG;
-      vr[u] = (jj < k1 && jj != p) ? *(const uint4*)(vh + (size_t)jj * DH + vd)
-                                   : make_uint4(0, 0, 0, 0);
+      const int jj = c + vr + u * VP;
+      vr4[u] = (jj < k1 && jj != p) ? *(const uint4*)(vh + (size_t)jj * DH + vd)
+                                    : make_uint4(0, 0, 0, 0);
     }
   };
-  uint4 ka[KU], va[VU];
-  if (k0 < k1) load_chunk(k0, ka, va);   // independent of q: overlaps the prologue
+  uint4 kb[AD_RING][KU], vb[AD_RING][VU];
+#pragma unroll
+  for (int r = 0; r < AD_RING - 1; ++r)
+    if (r < nt) load(r, kb[r], vb[r]);   // independent of q: overlaps the prologue
 
-  // ---- new token: QK-norm + RoPE (one dim pair per lane)
+  // ---- new token: QK-norm + RoPE (wave 0, one dim pair per lane)
   if (tid < P) {
     const bf16_t* row = qkv + (size_t)b * 3 * d + h * DH + 2 * tid;
     const uint32_t qw = *(const uint32_t*)row;
@@ -94,8 +106,8 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     float q0 = __uint_as_float(qw << 16), q1 = __uint_as_float(qw & 0xffff0000u);
     float c0 = __uint_as_float(kw << 16), c1 = __uint_as_float(kw & 0xffff0000u);
     const float sq = group_sum<P>(q0 * q0 + q1 * q1);
-    const float sk = group_sum<P>(c0 * c0 + c1 * c1);
-    const float rq = rsqrtf(sq / (float)DH + eps), rk = rsqrtf(sk / (float)DH + eps);
+    const float sk2 = group_sum<P>(c0 * c0 + c1 * c1);
+    const float rq = rsqrtf(sq / (float)DH + eps), rk = rsqrtf(sk2 / (float)DH + eps);
     q0 = rbf(q0 * rq); q1 = rbf(q1 * rq);
     c0 = rbf(c0 * rk); c1 = rbf(c1 * rk);
     if (tid < D4) {
@@ -104,107 +116,105 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
       const float b0 = c * c0 + s * c1, b1 = c * c1 - s * c0;
       q0 = a0; q1 = a1; c0 = b0; c1 = b1;
     }
-    q0 = rbf(q0); q1 = rbf(q1); c0 = rbf(c0); c1 = rbf(c1);
-    s_q[2 * tid] = q0; s_q[2 * tid + 1] = q1;
-    s_k[2 * tid] = c0; s_k[2 * tid + 1] = c1;
+    s_qp[tid] = pack2(q0, q1);
+    const uint32_t kp = pack2(c0, c1);
+    s_kp[tid] = kp;
     s_v[2 * tid] = __uint_as_float(vw << 16);
     s_v[2 * tid + 1] = __uint_as_float(vw & 0xffff0000u);
     if (k0 <= p && p < k1) {   // this work-group owns position p: append to the cache
       const size_t ci = (((size_t)b * H + h) * max_ctx + p) * DH + 2 * tid;
-      *(uint32_t*)(kc + ci) = pack2(c0, c1);
+      *(uint32_t*)(kc + ci) = kp;
       *(uint32_t*)(vc + ci) = vw;
     }
   }
   __syncthreads();
 
-  float qf[DPT];
+  uint32_t qp[DH / 8];   // this lane's Dh/4 score dims of q, as pairs
 #pragma unroll
-  for (int e = 0; e < DPT; ++e) qf[e] = s_q[qd + e];
+  for (int e = 0; e < DH / 8; ++e) qp[e] = s_qp[sd / 2 + e];
+  const float sl2 = scale * 1.4426950408889634f, sh2 = shift * 1.4426950408889634f;
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   float lsum = 0.f;
 
-  for (int c = k0; c < k1; c += AD_KC) {
-    uint4 kb[KU], vb[VU];
-    const bool more = c + AD_KC < k1;
-    if (more) load_chunk(c + AD_KC, kb, vb);   // next chunk in flight during this one
-    const int kn = min(AD_KC, k1 - c);
-    {
-      const int j = c + kk;
-      float s = 0.f;
-      if (kk < kn) {
-        if (j == p) {
+  auto compute = [&](int t, const uint4* kr, const uint4* vr4) {
+    const int c = chunk_base(t);
+    const int j = c + sk;
+    float s = 0.f;
+    if (j == p) {
 #pragma unroll
-          for (int e = 0; e < DPT; ++e) s += qf[e] * s_k[qd + e];
-        } else {
+      for (int e = 0; e < DH / 8; ++e) s = dot2_bf16(qp[e], s_kp[sd / 2 + e], s);
+    } else {
 #pragma unroll
-          for (int u = 0; u < KU; ++u) {
-            float kf[8];
-            unpack8(ka[u], kf);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s += qf[u * 8 + e] * kf[e];
-          }
-        }
+      for (int u = 0; u < KU; ++u) {
+        s = dot2_bf16(qp[4 * u + 0], kr[u].x, s);
+        s = dot2_bf16(qp[4 * u + 1], kr[u].y, s);
+        s = dot2_bf16(qp[4 * u + 2], kr[u].z, s);
+        s = dot2_bf16(qp[4 * u + 3], kr[u].w, s);
       }
-      s = group_sum<TPK>(s);
-      if (tid % TPK == 0) s_p[kk] = kk < kn ? expf(s * scale - shift) : 0.f;
     }
-    __syncthreads();
-    if (tid < AD_KC) lsum += s_p[tid];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    const float pj = j < k1 ? __builtin_amdgcn_exp2f(s * sl2 - sh2) : 0.f;
+    if ((lane & 3) == 0) lsum += pj;
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
-      const int kv = vg + u * NG;
-      if (kv < kn) {
-        const float pj = s_p[kv];
-        float vf[8];
-        if (c + kv == p) {
+      const int r = vr + u * VP;
+      const float pr = __shfl(pj, 4 * r, 64);
+      float vf[8];
+      if (c + r == p) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = s_v[vd + e];
-        } else {
-          unpack8(va[u], vf);
-        }
+        for (int e = 0; e < 8; ++e) vf[e] = s_v[vd + e];
+      } else {
+        unpack8(vr4[u], vf);
+      }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += pj * vf[e];
+      for (int e = 0; e < 8; ++e) acc[e] += pr * vf[e];
+    }
+  };
+
+  for (int t = 0; t < nt; t += AD_RING) {
+#pragma unroll
+    for (int r = 0; r < AD_RING; ++r) {
+      if (t + r < nt) {
+        const int tn = t + r + AD_RING - 1;
+        if (tn < nt) load(tn, kb[(r + AD_RING - 1) % AD_RING], vb[(r + AD_RING - 1) % AD_RING]);
+        compute(t + r, kb[r], vb[r]);
       }
     }
-    __syncthreads();
-    if (more) {
+  }
+
+  // ---- (O, L) of this work-group: lanes sharing dims, then waves in order
 #pragma unroll
-      for (int u = 0; u < KU; ++u) ka[u] = kb[u];
+  for (int o = VL; o < 64; o <<= 1)
 #pragma unroll
-      for (int u = 0; u < VU; ++u) va[u] = vb[u];
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  lsum = group_sum<64>(lsum);
+  if (lane < VL) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_o[wv][vd + e] = acc[e];
+  }
+  if (lane == 0) s_l[wv] = lsum;
+  __syncthreads();
+  float ot = 0.f, lt = 0.f;
+  if (tid < DH) {
+#pragma unroll
+    for (int w = 0; w < AD_THREADS / 64; ++w) {
+      ot += s_o[w][tid];
+      lt += s_l[w];
     }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) s_o[vg][vd + e] = acc[e];
-  lsum = group_sum<64>(lsum);
-  if ((tid & 63) == 0) s_l[tid >> 6] = lsum;
-  __syncthreads();
+  if (nsplit == 1) {   // the whole key range: o = O / L
+    if (tid < DH) out[(size_t)b * d + h * DH + tid] = f2bf(ot / lt);
+    return;
+  }
   // partial (O, L) of this split with coherent stores; the last split of
   // (b, h) to arrive sums all of them in split order and writes o = O / L
   float* pbase = part + ((size_t)b * H + h) * nsplit * (DH + 1);
   float* pp = pbase + (size_t)split * (DH + 1);
-  if (tid < DH) {
-    float o = 0.f;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) o += s_o[g][tid];
-    __hip_atomic_store(pp + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (tid == 0) {
-    float l = 0.f;
-    for (int w = 0; w < AD_THREADS / 64; ++w) l += s_l[w];
-    __hip_atomic_store(pp + DH, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (nsplit == 1) {
-    __syncthreads();
-    if (tid < DH) {
-      const float o = __hip_atomic_load(pp + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float l = __hip_atomic_load(pp + DH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[(size_t)b * d + h * DH + tid] = f2bf(o / l);
-    }
-    return;
-  }
+  if (tid < DH) __hip_atomic_store(pp + tid, ot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(pp + DH, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   __shared__ unsigned s_last;

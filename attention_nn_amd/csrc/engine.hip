@@ -220,15 +220,16 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   return ANN_OK;
 }
 
-// Split count of the decode attention: enough work-groups (about 1024) to
-// fill the GPU, at most one 64-key chunk per split of the longest key range.
+// Split count of the decode attention: about 384 work-groups (1.5 per CU:
+// more splits cost a partial round trip each and measured slower at batch
+// 64), at most one 64-key chunk per split of the longest key range.
 // Independent of the current length, so a captured step replays at every
 // position.
 int dec_splits(const ann_config& g, bool lng, int B) {
   const int keys = lng ? g.max_ctx : (g.window < g.max_ctx ? g.window : g.max_ctx);
   int n = (keys + 63) / 64;
   if (n > MAX_SPLIT) n = MAX_SPLIT;
-  const int want = (1024 + B * g.H - 1) / (B * g.H);
+  const int want = (384 + B * g.H - 1) / (B * g.H);
   if (n > want) n = want;
   return n < 1 ? 1 : n;
 }
