@@ -66,9 +66,10 @@ SIGNATURES = {
     "ann_op_rms_norm": (ctypes.c_int, [_P, _P, _I, _I, ctypes.c_float, _I, _P]),
     "ann_profile_enable": (ctypes.c_int, [_P, _I, _I]),
     "ann_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(_I)]),
+    "ann_check_device": (ctypes.c_int, [_P, _P]),
 }
 
-PROF_KINDS = {"lm_head": 0, "qkv": 1, "o": 2, "fc": 3, "proj": 4, "attn": 5}
+PROF_KINDS = {"lm_head": 0, "qkv": 1, "o": 2, "fc": 3, "proj": 4, "attn": 5, "step": 6}
 
 _lib = None
 

@@ -69,3 +69,26 @@ __device__ __forceinline__ float softcap(float z) {
   float t = (z + 5.0f) / 7.5f;
   return 23.0f * (1.0f / (1.0f + expf(-t)));
 }
+
+// Block epilogues of model.py, each eager op rounded to bf16 (y: fp32
+// accumulator of the projection, lam: the layer's r0 r1 p0 p1 x0l).
+//   x = ((r0 x) + (p0 y)) + (x0l x0)                          (model.py:255-256)
+__device__ __forceinline__ bf16_t mix_attn(const float* lam, float x, float x0, float y) {
+  const float yb = rbf(y);
+  const float t = rbf(rbf(lam[0] * x) + rbf(lam[2] * yb));
+  return f2bf(t + rbf(lam[4] * x0));
+}
+//   x = (r1 x) + (p1 y)                                        (model.py:259-260)
+__device__ __forceinline__ bf16_t mix_mlp(const float* lam, float x, float y) {
+  return f2bf(rbf(lam[1] * x) + rbf(lam[3] * rbf(y)));
+}
+//   relu(y)^2                                                  (model.py:258)
+__device__ __forceinline__ bf16_t relu2_bf(float y) {
+  const float u = rbf(y);
+  const float r = u > 0.f ? u : 0.f;
+  return f2bf(r * r);
+}
+// Order-preserving 16-bit key of a bf16 value (greedy argmax).
+__device__ __forceinline__ uint32_t zkey(bf16_t h) {
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
+}

@@ -1,0 +1,656 @@
+// Persistent decode step for batch 1: embed, every layer, lm_head and the
+// greedy argmax of one token in ONE cooperative launch of one 512-thread
+// work-group per CU (model.py:223-263 for T = 1, sample.py:44-49 greedy).
+//
+// Why: at batch 1 a decode step is ~57 dependent phases whose own work is a
+// few microseconds of weight streaming; as separate kernels every phase pays
+// a launch and a cold memory round trip.  Here the work-groups stay resident
+// and hand the small activation vectors to each other through LL exchanges:
+// every 64-bit word carries 32 bits of data and a 32-bit tag (step
+// generation * 256 + phase), written with one relaxed device-scope store and
+// polled with device-scope loads -- data and "ready" arrive together, no
+// fence and no barrier.  Each phase issues its weight (and K/V) loads before
+// it waits for its input, so their latency hides behind the exchange.
+//
+// Phases of layer l (tags 5l+1 .. 5l+5), rows of every projection split over
+// all work-groups in pairs (one tagged word = two bf16 outputs):
+//   1  qkv  = rms(x) Wqkv^T                       -> xq
+//   2  attention of (head h, split s): QK-norm, RoPE, cache append, softmax
+//      partial (O, L) with a fixed shift (|s| <= scale Dh) -> xp
+//   3  o = sum_s O_s / sum_s L_s; x' = mix_attn(x, x0, o Wo^T)  -> xm
+//   4  h = relu2(rms(x') Wfc^T)                   -> xh
+//   5  x = mix_mlp(x', h Wproj^T)                 -> xx
+// then z = rms(x) lm_head^T: greedy keys (bf16 order << 16 | 0xffff - n) per
+// work-group -> xk, work-group 0 picks the token and advances pos; otherwise
+// z is stored for the sampler kernel.
+//
+// Every wait is bounded: after PD_SPIN polls (or once any work-group has
+// flagged a timeout in *err) it gives up and the kernel runs to its end, so
+// all waves always exit; the host reports a set flag as an error.  The grid
+// must be co-resident (cooperative launch, one work-group per CU).
+#include <math.h>
+#include "common.h"
+#include "launch.h"
+
+namespace ann {
+
+constexpr int PD_T = 512;
+constexpr int PD_NW = PD_T / 64;
+constexpr int PD_SLOTS = 12;                 // 16-byte weight chunks per lane in flight
+constexpr int PD_RMAX = PD_NW * PD_SLOTS;    // projection rows per work-group (U = 1)
+constexpr int PD_KW = 16;                    // keys per wave chunk
+constexpr uint32_t PD_PH = 256;              // tags per step
+constexpr unsigned PD_SPIN = 1u << 18;
+
+typedef __bf16 pd_bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float pd_dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(pd_bf16x2, a),
+                                         __builtin_bit_cast(pd_bf16x2, b), c, false);
+}
+__device__ __forceinline__ float pd_dot8(const uint4& w, const uint4& x, float c) {
+  c = pd_dot2(w.x, x.x, c);
+  c = pd_dot2(w.y, x.y, c);
+  c = pd_dot2(w.z, x.z, c);
+  return pd_dot2(w.w, x.w, c);
+}
+
+__device__ __forceinline__ void ll_store(u64* p, uint32_t v, uint32_t tag) {
+  __hip_atomic_store(p, ((u64)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ll_load(const u64* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until the word carries `tag`; bounded (see the file comment).
+__device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
+  u64 v = ll_load(p);
+  unsigned s = 0;
+  while ((uint32_t)(v >> 32) != tag) {
+    ++s;
+    if ((s & 127u) == 0) {
+      if (s >= PD_SPIN) {
+        atomicOr(err, 1u);
+        break;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    v = ll_load(p);
+  }
+  return (uint32_t)v;
+}
+// dst[i] = data of src[i] for i < n, all loads of a thread issued first.
+__device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, uint32_t tag,
+                                        unsigned* err) {
+  for (int i0 = 0; i0 < n; i0 += PD_T * 8) {
+    u64 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + j * PD_T + (int)threadIdx.x;
+      v[j] = i < n ? ll_load(src + i) : 0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + j * PD_T + (int)threadIdx.x;
+      if (i < n) dst[i] = (uint32_t)(v[j] >> 32) == tag ? (uint32_t)v[j] : ll_wait(src + i, tag, err);
+    }
+  }
+}
+
+// Rows of a projection owned by work-group g: pairs [b, e) of npairs.
+__device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr) {
+  const int g = blockIdx.x, G = gridDim.x;
+  const int b = (int)((long long)npairs * g / G), e = (int)((long long)npairs * (g + 1) / G);
+  n0 = 2 * b;
+  nr = 2 * (e - b);
+}
+
+// Weight chunks of this lane: row n0 + wave + 8 rr, chunks lane + 64 u.
+template <int U>
+__device__ __forceinline__ void pd_wload(const bf16_t* W, int K, int n0, int nr, uint4* wr) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
+#pragma unroll
+  for (int rr = 0; rr < PD_SLOTS / U; ++rr) {
+    const int r = wv + PD_NW * rr;
+    const bool ok = r < nr;
+    const uint4* row = (const uint4*)(W + (size_t)(n0 + (ok ? r : 0)) * K);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = lane + 64 * u;
+      wr[rr * U + u] = (ok && c < K8) ? row[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
+// stage[b][r] = dot(row r, gin[b]) for the nr rows of this work-group.
+template <int U, int BM>
+__device__ __forceinline__ void pd_wdot(const uint4* wr, const uint4* gin, int K, int nr,
+                                        float (*stage)[PD_RMAX]) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
+#pragma unroll
+  for (int rr = 0; rr < PD_SLOTS / U; ++rr) {
+    const int r = wv + PD_NW * rr;
+    if (r < nr) {
+      float acc[BM];
+#pragma unroll
+      for (int b = 0; b < BM; ++b) acc[b] = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = lane + 64 * u;
+        if (c < K8) {
+#pragma unroll
+          for (int b = 0; b < BM; ++b) acc[b] = pd_dot8(wr[rr * U + u], gin[b * K8 + c], acc[b]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < BM; ++b) {
+        const float t = group_sum<64>(acc[b]);
+        if (lane == 0) stage[b][r] = t;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// dst = bf16(src * rsqrt(mean(src^2) + eps)) for BM rows of K (LDS to LDS).
+template <int BM>
+__device__ __forceinline__ void pd_rms(const bf16_t* src, bf16_t* dst, int K, float eps,
+                                       float (*red)[PD_NW]) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t* s2 = (const uint32_t*)src;
+  uint32_t* d2 = (uint32_t*)dst;
+  const int K2 = K >> 1;
+  float sc[BM];
+#pragma unroll
+  for (int b = 0; b < BM; ++b) {
+    float ss = 0.f;
+    for (int i = tid; i < K2; i += PD_T) {
+      const uint32_t w = s2[b * K2 + i];
+      const float a = __uint_as_float(w << 16), c = __uint_as_float(w & 0xffff0000u);
+      ss += a * a + c * c;
+    }
+    ss = group_sum<64>(ss);
+    if (lane == 0) red[b][wv] = ss;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < BM; ++b) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < PD_NW; ++w) t += red[b][w];
+    sc[b] = rsqrtf(t / (float)K + eps);
+  }
+#pragma unroll
+  for (int b = 0; b < BM; ++b)
+    for (int i = tid; i < K2; i += PD_T) {
+      const uint32_t w = s2[b * K2 + i];
+      d2[b * K2 + i] = pack2(__uint_as_float(w << 16) * sc[b], __uint_as_float(w & 0xffff0000u) * sc[b]);
+    }
+  __syncthreads();
+}
+
+enum { PE_STORE = 0, PE_ATTN = 1, PE_RELU2 = 2, PE_MLP = 3 };
+
+// Epilogue of this work-group's rows [n0, n0 + nr) and tagged stores of the
+// bf16 pairs to dst (row stride rw words).
+template <int E, int BM>
+__device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr, u64* dst, int rw,
+                                        uint32_t tag, const float* lam, const bf16_t* xr,
+                                        const bf16_t* x0, int d) {
+  const int np = nr >> 1;
+  for (int i = threadIdx.x; i < BM * np; i += PD_T) {
+    const int b = i / np, j = i - b * np, n = n0 + 2 * j;
+    const float y0 = stage[b][2 * j], y1 = stage[b][2 * j + 1];
+    uint32_t v;
+    if (E == PE_STORE) {
+      v = pack2(y0, y1);
+    } else if (E == PE_RELU2) {
+      v = (uint32_t)relu2_bf(y0) | ((uint32_t)relu2_bf(y1) << 16);
+    } else if (E == PE_ATTN) {
+      const bf16_t a = mix_attn(lam, bf2f(xr[b * d + n]), bf2f(x0[b * d + n]), y0);
+      const bf16_t c = mix_attn(lam, bf2f(xr[b * d + n + 1]), bf2f(x0[b * d + n + 1]), y1);
+      v = (uint32_t)a | ((uint32_t)c << 16);
+    } else {
+      const bf16_t a = mix_mlp(lam, bf2f(xr[b * d + n]), y0);
+      const bf16_t c = mix_mlp(lam, bf2f(xr[b * d + n + 1]), y1);
+      v = (uint32_t)a | ((uint32_t)c << 16);
+    }
+    ll_store(dst + (size_t)b * rw + (n >> 1), v, tag);
+  }
+}
+
+template <int DH, int BM, int UD>
+__global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
+  constexpr int KU = DH / 32;       // K slices per lane per chunk (4 lanes per key)
+  constexpr int VL = DH / 8;        // lanes per V row
+  constexpr int VP = 64 / VL;       // V rows per pass
+  constexpr int VU = PD_KW / VP;    // V passes per chunk
+  constexpr int P2 = DH / 2, D4 = DH / 4;
+  constexpr int PD_RING = DH == 128 ? 2 : 3;   // key chunks in flight per wave
+
+  extern __shared__ uint4 lds4[];
+  __shared__ float stage[BM][PD_RMAX];
+  __shared__ float red[BM][PD_NW];
+  __shared__ int s_pos[BM];
+  __shared__ uint32_t s_in[3 * P2];   // raw q, k, v pairs of one head
+  __shared__ uint32_t s_qp[P2];
+  __shared__ uint32_t s_kp[P2];
+  __shared__ float s_v[DH];
+  __shared__ float s_o[PD_NW][DH];
+  __shared__ float s_l[PD_NW];
+  __shared__ u64 s_key[BM][PD_NW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int G = gridDim.x, g = blockIdx.x;
+  const int d = P.d, H = P.H, d2 = d >> 1;
+  bf16_t* sx0 = (bf16_t*)lds4;        // x0 (BM x d)
+  bf16_t* sxs = sx0 + BM * d;         // layer input x
+  bf16_t* sxm = sxs + BM * d;         // x after attention
+  bf16_t* gin = sxm + BM * d;         // projection input (BM x 4d)
+  float* spart = (float*)(gin + BM * 4 * d);   // attention partials
+
+  const uint32_t tb = __hip_atomic_load(P.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * PD_PH;
+  if (tid < BM) s_pos[tid] = P.pos[tid];
+
+  // ---- x = x0 = rms(embed[tok]) (every work-group, redundantly)
+  for (int b = 0; b < BM; ++b) {
+    int t = P.tok[b];
+    t = t < 0 ? 0 : (t >= P.V ? P.V - 1 : t);
+    const uint32_t* e = (const uint32_t*)(P.emb + (size_t)t * d);
+    for (int i = tid; i < d2; i += PD_T) ((uint32_t*)gin)[b * d2 + i] = e[i];
+  }
+  __syncthreads();
+  pd_rms<BM>(gin, sx0, d, P.eps, red);
+  for (int i = tid; i < BM * d2; i += PD_T) ((uint32_t*)sxs)[i] = ((const uint32_t*)sx0)[i];
+  __syncthreads();
+
+  uint4 wr[PD_SLOTS];
+  for (int l = 0; l < P.L; ++l) {
+    const bf16_t* Wl = P.layers + P.lstride * l;
+    const float* lam = P.lam + 8 * l;
+    const bool lng = (P.long_mask >> l) & 1ull;
+    const uint32_t t1 = tb + 5u * l + 1u;
+    int n0, nr;
+
+    // ---- 1: qkv
+    pd_rows(3 * d2, n0, nr);
+    pd_wload<UD>(Wl + P.o_qkv, d, n0, nr, wr);
+    if (l > 0) {
+      ll_poll(P.xx, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
+      __syncthreads();
+    }
+    pd_rms<BM>(sxs, gin, d, P.eps, red);
+    pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+    pd_emit<PE_STORE, BM>(stage, n0, nr, P.xq, 3 * d2, t1, lam, nullptr, nullptr, d);
+
+    // ---- 2: attention of (b, h, split)
+    pd_rows(d2, n0, nr);
+    const int S = lng ? P.s_long : P.s_win;
+    const bool attn = g < BM * H * S;
+    // o projection weights for phase 3: now on work-groups without attention,
+    // after it on the others (keeps the K/V ring and these apart)
+    if (!attn) pd_wload<UD>(Wl + P.o_o, d, n0, nr, wr);
+    if (attn) {
+      const int s = g % S, h = (g / S) % H, b = g / (S * H);
+      const int p = s_pos[b];
+      const int lo = lng ? 0 : max(0, p - P.window + 1);
+      const int n = p - lo + 1;
+      const int per = (n + S - 1) / S;
+      const int k0 = lo + s * per;
+      const int k1 = min(p + 1, k0 + per);
+      const int nch = k1 > k0 ? (k1 - k0 + PD_KW - 1) / PD_KW : 0;
+      const int nt = nch > wv ? (nch - wv + PD_NW - 1) / PD_NW : 0;
+      const size_t ho = (((size_t)b * H + h) * P.max_ctx) * DH;
+      bf16_t* kcl = P.kc + P.kvl * l;
+      bf16_t* vcl = P.vc + P.kvl * l;
+      const bf16_t* kh = kcl + ho;
+      const bf16_t* vh = vcl + ho;
+      const int sk = lane >> 2, sd = (lane & 3) * (DH / 4);
+      const int vr = lane / VL, vd = (lane % VL) * 8;
+      auto cbase = [&](int t) { return k0 + PD_KW * (wv + PD_NW * t); };
+      auto load = [&](int t, uint4* kr, uint4* vr4) {
+        const int c = cbase(t);
+        const int j = c + sk;
+        const bool ok = j < k1 && j != p;
+#pragma unroll
+        for (int u = 0; u < KU; ++u)
+          kr[u] = ok ? *(const uint4*)(kh + (size_t)j * DH + sd + u * 8) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+          const int jj = c + vr + u * VP;
+          vr4[u] = (jj < k1 && jj != p) ? *(const uint4*)(vh + (size_t)jj * DH + vd)
+                                        : make_uint4(0u, 0u, 0u, 0u);
+        }
+      };
+      uint4 kb[PD_RING][KU], vb[PD_RING][VU];
+#pragma unroll
+      for (int r = 0; r < PD_RING - 1; ++r)
+        if (r < nt) load(r, kb[r], vb[r]);
+      // q, k, v of this head from phase 1
+      const u64* src = P.xq + (size_t)b * 3 * d2 + h * P2;
+      for (int i = tid; i < 3 * P2; i += PD_T) {
+        const int part = i / P2, k = i - part * P2;
+        s_in[i] = ll_wait(src + part * d2 + k, t1, P.err);
+      }
+      __syncthreads();
+      if (tid < P2) {   // QK-norm + RoPE, one dim pair per lane
+        const uint32_t qw = s_in[tid], kw = s_in[P2 + tid], vw = s_in[2 * P2 + tid];
+        float q0 = __uint_as_float(qw << 16), q1 = __uint_as_float(qw & 0xffff0000u);
+        float c0 = __uint_as_float(kw << 16), c1 = __uint_as_float(kw & 0xffff0000u);
+        const float sq = group_sum<P2>(q0 * q0 + q1 * q1);
+        const float sk2 = group_sum<P2>(c0 * c0 + c1 * c1);
+        const float rq = rsqrtf(sq / (float)DH + P.eps), rk = rsqrtf(sk2 / (float)DH + P.eps);
+        q0 = rbf(q0 * rq); q1 = rbf(q1 * rq);
+        c0 = rbf(c0 * rk); c1 = rbf(c1 * rk);
+        if (tid < D4) {
+          const float c = P.cs[(size_t)p * D4 + tid], sn = P.sn[(size_t)p * D4 + tid];
+          const float a0 = c * q0 + sn * q1, a1 = c * q1 - sn * q0;
+          const float b0 = c * c0 + sn * c1, b1 = c * c1 - sn * c0;
+          q0 = a0; q1 = a1; c0 = b0; c1 = b1;
+        }
+        s_qp[tid] = pack2(q0, q1);
+        const uint32_t kp = pack2(c0, c1);
+        s_kp[tid] = kp;
+        s_v[2 * tid] = __uint_as_float(vw << 16);
+        s_v[2 * tid + 1] = __uint_as_float(vw & 0xffff0000u);
+        if (k0 <= p && p < k1) {   // this split owns p: append to the cache
+          const size_t ci = ho + (size_t)p * DH + 2 * tid;
+          *(uint32_t*)(kcl + ci) = kp;
+          *(uint32_t*)(vcl + ci) = vw;
+        }
+      }
+      __syncthreads();
+      uint32_t qp[DH / 8];
+#pragma unroll
+      for (int e = 0; e < DH / 8; ++e) qp[e] = s_qp[sd / 2 + e];
+      const float sl2 = P.scale * 1.4426950408889634f, sh2 = P.shift * 1.4426950408889634f;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+      float lsum = 0.f;
+      auto compute = [&](int t, const uint4* kr, const uint4* vr4) {
+        const int c = cbase(t);
+        const int j = c + sk;
+        float sc = 0.f;
+        if (j == p) {
+#pragma unroll
+          for (int e = 0; e < DH / 8; ++e) sc = pd_dot2(qp[e], s_kp[sd / 2 + e], sc);
+        } else {
+#pragma unroll
+          for (int u = 0; u < KU; ++u) {
+            sc = pd_dot2(qp[4 * u + 0], kr[u].x, sc);
+            sc = pd_dot2(qp[4 * u + 1], kr[u].y, sc);
+            sc = pd_dot2(qp[4 * u + 2], kr[u].z, sc);
+            sc = pd_dot2(qp[4 * u + 3], kr[u].w, sc);
+          }
+        }
+        sc += __shfl_xor(sc, 1, 64);
+        sc += __shfl_xor(sc, 2, 64);
+        const float pj = j < k1 ? __builtin_amdgcn_exp2f(sc * sl2 - sh2) : 0.f;
+        if ((lane & 3) == 0) lsum += pj;
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+          const int r = vr + u * VP;
+          const float pr = __shfl(pj, 4 * r, 64);
+          float vf[8];
+          if (c + r == p) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vf[e] = s_v[vd + e];
+          } else {
+            unpack8(vr4[u], vf);
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += pr * vf[e];
+        }
+      };
+      for (int t = 0; t < nt; t += PD_RING) {
+#pragma unroll
+        for (int r = 0; r < PD_RING; ++r) {
+          if (t + r < nt) {
+            const int tn = t + r + PD_RING - 1;
+            if (tn < nt) load(tn, kb[(r + PD_RING - 1) % PD_RING], vb[(r + PD_RING - 1) % PD_RING]);
+            compute(t + r, kb[r], vb[r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int o = VL; o < 64; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+      lsum = group_sum<64>(lsum);
+      if (lane < VL) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_o[wv][vd + e] = acc[e];
+      }
+      if (lane == 0) s_l[wv] = lsum;
+      __syncthreads();
+      u64* dst = P.xp + (size_t)g * (DH + 1);   // g = (b * H + h) * S + s
+      if (tid < DH) {
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < PD_NW; ++w) o += s_o[w][tid];
+        ll_store(dst + tid, __float_as_uint(o), t1 + 1u);
+      }
+      if (tid == 0) {
+        float lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < PD_NW; ++w) lt += s_l[w];
+        ll_store(dst + DH, __float_as_uint(lt), t1 + 1u);
+      }
+      pd_wload<UD>(Wl + P.o_o, d, n0, nr, wr);
+    }
+
+    // ---- 3: o = combine(partials); x' = mix_attn(x, x0, o Wo^T)
+    {
+      const int nw = BM * H * S * (DH + 1);
+      ll_poll(P.xp, nw, (uint32_t*)spart, t1 + 1u, P.err);
+      __syncthreads();
+      for (int i = tid; i < BM * d; i += PD_T) {
+        const int b = i / d, c = i - b * d, h = c / DH, e = c - h * DH;
+        const float* pb = spart + (size_t)((b * H + h) * S) * (DH + 1);
+        float o = 0.f, lt = 0.f;
+        for (int s = 0; s < S; ++s) {
+          o += pb[s * (DH + 1) + e];
+          lt += pb[s * (DH + 1) + DH];
+        }
+        gin[i] = f2bf(o / lt);
+      }
+      __syncthreads();
+      pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+      pd_emit<PE_ATTN, BM>(stage, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d);
+    }
+
+    // ---- 4: h = relu2(rms(x') Wfc^T)
+    pd_rows(2 * d, n0, nr);
+    pd_wload<UD>(Wl + P.o_fc, d, n0, nr, wr);
+    ll_poll(P.xm, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
+    __syncthreads();
+    pd_rms<BM>(sxm, gin, d, P.eps, red);
+    pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+    pd_emit<PE_RELU2, BM>(stage, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr, nullptr, d);
+
+    // ---- 5: x = mix_mlp(x', h Wproj^T)
+    pd_rows(d2, n0, nr);
+    pd_wload<4 * UD>(Wl + P.o_proj, 4 * d, n0, nr, wr);
+    ll_poll(P.xh, BM * 2 * d, (uint32_t*)gin, t1 + 3u, P.err);
+    __syncthreads();
+    pd_wdot<4 * UD, BM>(wr, (const uint4*)gin, 4 * d, nr, stage);
+    pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d);
+  }
+
+  // ---- lm_head over this work-group's rows [r0, r1), two register batches
+  const uint32_t tl = tb + 5u * P.L;   // tag of the last x
+  const int r0 = (int)((long long)P.V * g / G), r1 = (int)((long long)P.V * (g + 1) / G);
+  constexpr int RB = PD_SLOTS / UD;    // rows per wave per batch
+  const int nrow = r1 - r0, nb = (nrow + PD_NW * RB - 1) / (PD_NW * RB);
+  const int K8 = d >> 3;
+  auto hload = [&](int k, uint4* w) {
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr) {
+      const int r = k * PD_NW * RB + wv + PD_NW * rr;
+      const bool ok = r < nrow;
+      const uint4* row = (const uint4*)(P.head + (size_t)(r0 + (ok ? r : 0)) * d);
+#pragma unroll
+      for (int u = 0; u < UD; ++u) {
+        const int c = lane + 64 * u;
+        w[rr * UD + u] = (ok && c < K8) ? row[c] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  u64 best[BM];
+#pragma unroll
+  for (int b = 0; b < BM; ++b) best[b] = 0ull;
+  auto hdot = [&](int k, const uint4* w) {
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr) {
+      const int r = k * PD_NW * RB + wv + PD_NW * rr;
+      if (r < nrow) {
+        const int n = r0 + r;
+        float acc[BM];
+#pragma unroll
+        for (int b = 0; b < BM; ++b) acc[b] = 0.f;
+#pragma unroll
+        for (int u = 0; u < UD; ++u) {
+          const int c = lane + 64 * u;
+          if (c < K8) {
+#pragma unroll
+            for (int b = 0; b < BM; ++b)
+              acc[b] = pd_dot8(w[rr * UD + u], ((const uint4*)gin)[b * K8 + c], acc[b]);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < BM; ++b) {
+          const float y = group_sum<64>(acc[b]);
+          const bf16_t zb = f2bf(y);
+          if (P.greedy) {
+            const u64 key = n < P.Vs ? (((u64)zkey(zb) << 16) | (u64)(0xffffu - (uint32_t)n)) : 0ull;
+            best[b] = key > best[b] ? key : best[b];
+          } else if (lane == 0) {
+            P.z[(size_t)b * P.V + n] = zb;
+          }
+          if (P.logits && lane == 0) P.logits[(size_t)b * P.V + n] = softcap(bf2f(zb));
+        }
+      }
+    }
+  };
+  uint4 wa[PD_SLOTS], wb[PD_SLOTS];
+  if (nb > 0) hload(0, wa);
+  ll_poll(P.xx, BM * d2, (uint32_t*)sxs, tl, P.err);
+  __syncthreads();
+  pd_rms<BM>(sxs, gin, d, P.eps, red);
+  for (int k = 0; k < nb; k += 2) {
+    if (k + 1 < nb) hload(k + 1, wb);
+    hdot(k, wa);
+    if (k + 1 < nb) {
+      if (k + 2 < nb) hload(k + 2, wa);
+      hdot(k + 1, wb);
+    }
+  }
+
+  if (P.greedy) {
+    if (lane == 0) {
+#pragma unroll
+      for (int b = 0; b < BM; ++b) s_key[b][wv] = best[b];
+    }
+    __syncthreads();
+    if (tid < BM) {
+      u64 m = 0;
+#pragma unroll
+      for (int w = 0; w < PD_NW; ++w) m = s_key[tid][w] > m ? s_key[tid][w] : m;
+      ll_store(P.xk + (size_t)g * BM + tid, (uint32_t)m, tl + 1u);
+    }
+    if (g == 0) {   // token = largest key over all work-groups
+      u64 m[BM];
+#pragma unroll
+      for (int b = 0; b < BM; ++b) m[b] = 0ull;
+      for (int i = tid; i < G; i += PD_T) {
+#pragma unroll
+        for (int b = 0; b < BM; ++b) {
+          const u64 v = ll_wait(P.xk + (size_t)i * BM + b, tl + 1u, P.err);
+          m[b] = v > m[b] ? v : m[b];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int b = 0; b < BM; ++b) {
+        u64 v = m[b];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const u64 w = (u64)__shfl_xor((unsigned)v, o, 64);
+          v = w > v ? w : v;
+        }
+        if (lane == 0) s_key[b][wv] = v;
+      }
+      __syncthreads();
+      if (tid < BM) {
+        u64 v = 0;
+#pragma unroll
+        for (int w = 0; w < PD_NW; ++w) v = s_key[tid][w] > v ? s_key[tid][w] : v;
+        P.out_tok[tid] = (int32_t)(0xffffu - (uint32_t)(v & 0xffffu));
+        P.pos[tid] = s_pos[tid] + 1;
+      }
+    }
+  }
+  // every work-group read the generation before its first output and work-
+  // group 0 has consumed outputs of all of them: advance it for the next step
+  if (g == 0 && tid == 0)
+    __hip_atomic_store(P.gen, (tb / PD_PH) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- host side --------------------------------------------------------------
+
+int decode_persist_slots(int d) { return d <= 512 ? 1 : d <= 1024 ? 2 : d <= 1536 ? 3 : 0; }
+
+bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long) {
+  const int ud = decode_persist_slots(d);
+  if (B != 1 || ud == 0 || (Dh != 64 && Dh != 128) || d % 16 || V % 2 || V > 65536 || L > 50 ||
+      G < 1)
+    return false;
+  const int d2 = d / 2;
+  auto rows = [&](int npairs) { return 2 * ((npairs + G - 1) / G); };
+  if (rows(3 * d2) > PD_NW * (PD_SLOTS / ud)) return false;
+  if (rows(d2) > PD_NW * (PD_SLOTS / ud)) return false;
+  if (rows(2 * d) > PD_NW * (PD_SLOTS / ud)) return false;
+  if (PD_SLOTS / (4 * ud) < 1 || rows(d2) > PD_NW * (PD_SLOTS / (4 * ud))) return false;
+  if (B * H * s_long > G || s_long < 1) return false;
+  return true;
+}
+
+size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
+  return (size_t)7 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
+}
+
+template <int DH, int BM, int UD>
+static hipError_t pd_launch(const PDParams& P, int G, size_t lds, hipStream_t st) {
+  const void* fn = (const void*)k_decode_persist<DH, BM, UD>;
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)(144 * 1024));
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  int nb = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, PD_T, lds);
+  if (e != hipSuccess) return e;
+  if (nb < 1) return hipErrorCooperativeLaunchTooLarge;
+  PDParams a = P;
+  void* args[] = {&a};
+  return hipLaunchCooperativeKernel(fn, dim3(G), dim3(PD_T), args, (unsigned)lds, st);
+}
+
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, hipStream_t st) {
+  const size_t lds = decode_persist_lds(B, P.d, P.H, Dh, P.s_long);
+  if (lds > 144 * 1024 || B != 1) return hipErrorInvalidValue;
+  switch (Dh * 16 + decode_persist_slots(P.d)) {
+    case 64 * 16 + 1: return pd_launch<64, 1, 1>(P, G, lds, st);
+    case 64 * 16 + 2: return pd_launch<64, 1, 2>(P, G, lds, st);
+    case 64 * 16 + 3: return pd_launch<64, 1, 3>(P, G, lds, st);
+    case 128 * 16 + 1: return pd_launch<128, 1, 1>(P, G, lds, st);
+    case 128 * 16 + 2: return pd_launch<128, 1, 2>(P, G, lds, st);
+    case 128 * 16 + 3: return pd_launch<128, 1, 3>(P, G, lds, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ann

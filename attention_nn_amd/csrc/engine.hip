@@ -74,8 +74,26 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, total;
+  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes, total;
 };
+
+// Exchange area of the persistent decode step (batch 1): tagged words of
+// xq, xp, xm, xh, xx, xk, then the generation and error words.  With
+// `which` = 1..8 returns the byte offset of that part, 0 the total size.
+constexpr int PD_BATCH = 1;
+constexpr int PD_MAX_SLONG = 8;
+constexpr int PD_MAX_G = 1024;
+size_t pd_layout(const ann_config& c, int which) {
+  const size_t d = c.d, H = c.H, Dh = d / c.H, B = PD_BATCH;
+  const size_t parts[8] = {B * 3 * d / 2, B * H * PD_MAX_SLONG * (Dh + 1), B * d / 2, B * 2 * d,
+                           B * d / 2, (size_t)PD_MAX_G * B, 1, 1};
+  size_t off = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (which == i + 1) return off;
+    off += up(parts[i] * 8);
+  }
+  return off;
+}
 
 SLayout ws_layout(const ann_config& c) {
   const size_t d = c.d, M = c.max_tokens, B = c.max_batch, Dh = d / c.H;
@@ -95,6 +113,7 @@ SLayout ws_layout(const ann_config& c) {
   s.hid = off; off += up(M * 4 * d * 2);
   s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
   s.zb = off; off += up(B * (size_t)c.V * 2);
+  s.pd = off; off += (s.pd_bytes = up(pd_layout(c, 0)));
   s.total = off;
   return s;
 }
@@ -159,6 +178,10 @@ struct ann_ctx {
   float sp_temp = 0.f;
   int sp_topk = 0;
   uint64_t sp_seed = 0, sp_step = 0;
+  // persistent batch-1 decode step
+  int n_cu = -1;         // CUs of the device (queried on first use)
+  bool pd_env = true;    // ANN_PERSIST=0 disables
+  bool pd_clear = true;  // exchange area must be cleared before the next use
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -369,8 +392,91 @@ void drop_graph(ann_ctx* c) {
   c->graph = nullptr;
 }
 
+int pd_splits(const ann_ctx* c, int B) {
+  int s = (c->c.max_ctx + 383) / 384;
+  if (s > PD_MAX_SLONG) s = PD_MAX_SLONG;
+  if (c->n_cu > 0 && s > c->n_cu / (B * c->c.H)) s = c->n_cu / (B * c->c.H);
+  return s < 1 ? 1 : s;
+}
+
+// Whether this decode step runs as the persistent kernel.
+bool persist_ok(ann_ctx* c, int B) {
+  if (!c->pd_env || B != PD_BATCH || (c->prof_kind >= 0 && c->prof_kind != ANN_PROF_STEP))
+    return false;
+  if (c->n_cu < 0) {
+    int dev = 0, n = 0, coop = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
+      n = 0;
+    c->n_cu = (coop && n <= PD_MAX_G) ? n : 0;
+  }
+  const ann_config& g = c->c;
+  return c->n_cu > 0 && g.n_long <= 8 &&
+         decode_persist_fits(B, g.d, g.H, c->Dh, g.V, g.L, c->n_cu, pd_splits(c, B));
+}
+
+int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
+                    float* logits, hipStream_t st) {
+  const ann_config& g = c->c;
+  PDParams P{};
+  P.emb = c->wptr(c->wl.embed);
+  P.head = c->wptr(c->wl.head);
+  P.layers = c->layer_w(0, 0);
+  P.lstride = c->wl.layer_stride / 2;
+  P.o_qkv = c->wl.qkv / 2;
+  P.o_o = c->wl.o / 2;
+  P.o_fc = c->wl.fc / 2;
+  P.o_proj = c->wl.proj / 2;
+  P.lam = (const float*)(c->w + c->wl.lam);
+  P.cs = (const float*)(c->w + c->wl.cs);
+  P.sn = (const float*)(c->w + c->wl.sn);
+  P.kc = c->kcache(0);
+  P.vc = c->vcache(0);
+  P.kvl = kv_layer_bytes(g) / 2;
+  P.long_mask = 0;
+  for (int i = 0; i < g.n_long; ++i) P.long_mask |= 1ull << g.long_layers[i];
+  P.tok = tokens;
+  P.out_tok = out_tok;
+  P.pos = c->sp<int32_t>(c->sl.pos);
+  P.z = c->sp<bf16_t>(c->sl.zb);
+  P.logits = logits;
+  uint8_t* pd = c->ws + c->sl.pd;
+  P.xq = (u64*)(pd + pd_layout(g, 1));
+  P.xp = (u64*)(pd + pd_layout(g, 2));
+  P.xm = (u64*)(pd + pd_layout(g, 3));
+  P.xh = (u64*)(pd + pd_layout(g, 4));
+  P.xx = (u64*)(pd + pd_layout(g, 5));
+  P.xk = (u64*)(pd + pd_layout(g, 6));
+  P.gen = (unsigned*)(pd + pd_layout(g, 7));
+  P.err = (unsigned*)(pd + pd_layout(g, 8));
+  P.d = g.d;
+  P.H = g.H;
+  P.L = g.L;
+  P.V = g.V;
+  P.Vs = g.V_sample;
+  P.max_ctx = g.max_ctx;
+  P.window = g.window;
+  P.s_win = 1;
+  P.s_long = pd_splits(c, B);
+  P.greedy = greedy ? 1 : 0;
+  P.scale = g.attn_scale;
+  P.shift = g.attn_scale * (float)c->Dh * 1.02f;
+  P.eps = g.rms_eps;
+  {
+    ProfScope ps(c, ANN_PROF_STEP, st);
+    HIPCHK(decode_persist(P, B, c->Dh, c->n_cu, st));
+  }
+  if (!greedy)
+    HIPCHK(sample(c->sp<bf16_t>(c->sl.zb), g.V, B, g.V_sample, c->sp<SampParams>(c->sl.sp),
+                  c->sp<unsigned long long>(c->sl.steps), out_tok, c->sp<int32_t>(c->sl.pos), 1,
+                  st));
+  return ANN_OK;
+}
+
 int enqueue_decode(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
                    float* logits, hipStream_t st) {
+  if (persist_ok(c, B)) return enqueue_persist(c, tokens, B, greedy, out_tok, logits, st);
   int rc = run_body(c, tokens, B, 1, st);
   if (rc) return rc;
   return head_and_sample(c, B, 1, greedy, out_tok, logits, 1, st);
@@ -421,6 +527,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->sl = ws_layout(*cfg);
   const char* ge = getenv("ANN_DECODE_GRAPH");
   c->use_graph = !(ge && ge[0] == '0');
+  const char* pe = getenv("ANN_PERSIST");
+  c->pd_env = !(pe && pe[0] == '0');
   *out = c;
   return ANN_OK;
 }
@@ -435,7 +543,7 @@ void ann_destroy(ann_ctx* ctx) {
 
 int ann_profile_enable(ann_ctx* c, int32_t kind, int32_t max_launches) {
   if (!c) return fail(ANN_E_ARG, "context is null");
-  if (kind < -1 || kind > ANN_PROF_ATTN) return fail(ANN_E_ARG, "bad kernel kind %d", kind);
+  if (kind < -1 || kind > ANN_PROF_STEP) return fail(ANN_E_ARG, "bad kernel kind %d", kind);
   for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   c->prof_ev.clear();
   c->prof_used = 0;
@@ -460,6 +568,21 @@ int ann_profile_read(ann_ctx* c, float* total_ms, int32_t* launches) {
   *total_ms = (float)tot;
   *launches = (int32_t)(c->prof_used / 2);
   c->prof_used = 0;
+  return ANN_OK;
+}
+
+int ann_check_device(ann_ctx* c, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  if (c->pd_clear) return ANN_OK;   // the persistent step has not run since binding
+  unsigned* err = (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8));
+  unsigned h = 0;
+  HIPCHK(hipMemcpy(&h, err, sizeof h, hipMemcpyDeviceToHost));
+  if (h) {
+    HIPCHK(hipMemset(err, 0, sizeof h));
+    return fail(ANN_E_HIP, "persistent decode: a cross-work-group wait timed out");
+  }
   return ANN_OK;
 }
 
@@ -526,6 +649,7 @@ int ann_bind(ann_ctx* c, void* wbuf, size_t wbytes, void* kv, size_t kvbytes, vo
   c->w = (uint8_t*)wbuf;
   c->kv = (uint8_t*)kv;
   c->ws = (uint8_t*)workspace;
+  c->pd_clear = true;
   c->bound = true;
   c->len = 0;
   c->B = 0;
@@ -614,6 +738,10 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   rc = sync_sampling(c, s, B, st);
   if (rc) return rc;
   const bool greedy = s->temperature == 0.f;
+  if (c->pd_clear && persist_ok(c, B)) {   // tags start from a clean area
+    HIPCHK(hipMemsetAsync(c->ws + c->sl.pd, 0, c->sl.pd_bytes, st));
+    c->pd_clear = false;
+  }
   if (c->use_graph && c->prof_kind < 0)
     rc = decode_graph(c, tokens, B, greedy, out_tok, logits, st);
   else

@@ -108,6 +108,42 @@ hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float 
 hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st);
 hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st);
 
+// Persistent decode step (batch 1): one cooperative launch of G work-groups
+// runs embed, all layers, lm_head and (greedy) the argmax; see
+// decode_persist.hip.  Exchange words are 64-bit (tag << 32 | data).
+typedef unsigned long long u64;
+struct PDParams {
+  const bf16_t* emb;
+  const bf16_t* head;
+  const bf16_t* layers;   // layer 0; layer l at layers + l * lstride
+  size_t lstride, o_qkv, o_o, o_fc, o_proj;   // elements
+  const float* lam;       // (L, 8): r0 r1 p0 p1 x0l
+  const float* cs;
+  const float* sn;
+  bf16_t* kc;             // caches of layer 0; layer l at + l * kvl
+  bf16_t* vc;
+  size_t kvl;
+  u64 long_mask;
+  const int32_t* tok;
+  int32_t* out_tok;
+  int32_t* pos;
+  bf16_t* z;              // !greedy: bf16 logits (B, V)
+  float* logits;          // optional fp32 softcapped logits (B, V)
+  u64* xq;                // qkv       B x 3d/2 words
+  u64* xp;                // partials  B*H*s_long x (Dh+1)
+  u64* xm;                // x'        B x d/2
+  u64* xh;                // hidden    B x 2d
+  u64* xx;                // x         B x d/2
+  u64* xk;                // keys      G x B
+  unsigned* gen;          // step generation (tags)
+  unsigned* err;          // set when a bounded wait timed out
+  int d, H, L, V, Vs, max_ctx, window, s_win, s_long, greedy;
+  float scale, shift, eps;
+};
+bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
+size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, hipStream_t st);
+
 hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st);
 hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,
                    int D, int pos0, int inverse, int dtype, hipStream_t st);

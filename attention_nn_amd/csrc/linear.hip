@@ -21,18 +21,13 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
   if (EPI == EPI_STORE) {
     ea.out[(size_t)m * ea.ldo + n] = f2bf(y);
   } else if (EPI == EPI_RELU2) {
-    float u = rbf(y);
-    float r = u > 0.f ? u : 0.f;
-    ea.out[(size_t)m * ea.ldo + n] = f2bf(r * r);
+    ea.out[(size_t)m * ea.ldo + n] = relu2_bf(y);
   } else if (EPI == EPI_RESID_ATTN) {
     const size_t i = (size_t)m * ea.ldr + n;
-    float yb = rbf(y);
-    float t = rbf(rbf(ea.lam[0] * bf2f(ea.x[i])) + rbf(ea.lam[2] * yb));
-    ea.x[i] = f2bf(t + rbf(ea.lam[4] * bf2f(ea.x0[i])));
+    ea.x[i] = mix_attn(ea.lam, bf2f(ea.x[i]), bf2f(ea.x0[i]), y);
   } else if (EPI == EPI_RESID_MLP) {
     const size_t i = (size_t)m * ea.ldr + n;
-    float yb = rbf(y);
-    ea.x[i] = f2bf(rbf(ea.lam[1] * bf2f(ea.x[i])) + rbf(ea.lam[3] * yb));
+    ea.x[i] = mix_mlp(ea.lam, bf2f(ea.x[i]), y);
   } else {  // EPI_LOGITS
     const bf16_t z = f2bf(y);
     const size_t i = (size_t)m * ea.ldz + n;
@@ -44,10 +39,6 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
 // ---- GEMV -------------------------------------------------------------------
 
 constexpr int GEMV_THREADS = 256;
-
-__device__ __forceinline__ uint32_t zkey(bf16_t h) {  // order-preserving 16-bit key
-  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
-}
 
 // Fill the LDS activation tile xs (M x K bf16) per the prologue PRE.
 template <int M, int PRE>

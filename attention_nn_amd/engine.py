@@ -100,7 +100,8 @@ class Engine:
 
     def profile(self, kind, max_launches=4096):
         """Bracket every launch of one kernel class ('lm_head', 'qkv', 'o',
-        'fc', 'proj', 'attn') with HIP events; None disables."""
+        'fc', 'proj', 'attn', or 'step' = the persistent batch-1 decode
+        kernel) with HIP events; None disables."""
         k = -1 if kind is None else _lib.PROF_KINDS[kind]
         _lib.check(_lib.lib().ann_profile_enable(self._ctx, k, int(max_launches)))
 
@@ -110,6 +111,11 @@ class Engine:
         n = ctypes.c_int32()
         _lib.check(_lib.lib().ann_profile_read(self._ctx, ctypes.byref(ms), ctypes.byref(n)))
         return ms.value, n.value
+
+    def check_device(self):
+        """Raise if a bounded cross-work-group wait of the persistent decode
+        step timed out since the last check (synchronises the stream)."""
+        _lib.check(_lib.lib().ann_check_device(self._ctx, _stream()))
 
     def reset(self):
         _lib.check(_lib.lib().ann_reset(self._ctx))

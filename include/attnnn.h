@@ -172,8 +172,15 @@ int ann_op_rms_norm(const void* x, void* y, int32_t rows, int32_t dim, float eps
 #define ANN_PROF_FC 3
 #define ANN_PROF_PROJ 4
 #define ANN_PROF_ATTN 5
+#define ANN_PROF_STEP 6   /* the persistent batch-1 decode kernel (whole step) */
 int ann_profile_enable(ann_ctx* ctx, int32_t kind, int32_t max_launches);
 int ann_profile_read(ann_ctx* ctx, float* total_ms, int32_t* launches);
+
+/* Device status of the persistent batch-1 decode step (no reference
+ * counterpart).  Its cross-work-group waits are bounded; one that gives up
+ * sets a device flag and the step's output is not valid.  Synchronises
+ * `stream`, returns ANN_E_HIP (and clears the flag) if it is set, else ANN_OK. */
+int ann_check_device(ann_ctx* ctx, void* stream);
 
 #ifdef __cplusplus
 }

@@ -139,6 +139,62 @@ def test_decode_teacher_forced_past_window(name, B):
     assert worst < LOGIT_TOL, worst
 
 
+@pytest.mark.parametrize("name", ["dh64", "dh128"])
+def test_persistent_decode_matches_oracle(name):
+    """Batch-1 decode runs as the single persistent kernel (tagged exchanges
+    between work-groups); its logits at every position, past the window, match
+    the oracle, and no bounded wait timed out."""
+    cfg = small_cfgs()[name]
+    p = perturb_lambdas(init_params(cfg, 15, dense=True))
+    T0, steps = 5, cfg.seq_len - 5
+    tok = np.random.default_rng(11).integers(0, cfg.vocab_size, (1, T0 + steps))
+    eng = _engine(cfg, p, 1)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :T0], want_logits=True)
+    ref = R.forward(prep, tok[:, :T0], cache)[:, -1]
+    worst = (lg.cpu() - ref).abs().max().item()
+    for i in range(steps - 1):
+        t = tok[:, T0 + i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
+    assert worst < LOGIT_TOL, worst
+
+
+def test_persistent_matches_kernel_path(monkeypatch):
+    """The persistent batch-1 step and the per-kernel step (ANN_PERSIST=0)
+    agree: greedy tokens identical over 60 steps, logits within the oracle
+    tolerance (the two sum the projections in different orders, so z can
+    differ by one bf16 ulp), and a seeded top-k draw sequence identical."""
+    cfg = small_cfgs()["dh128"]
+    p = perturb_lambdas(init_params(cfg, 21, dense=True))
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, (1, 6))
+
+    def run(persist, temp, k):
+        if not persist:
+            monkeypatch.setenv("ANN_PERSIST", "0")
+        eng = _engine(cfg, p, 1)
+        monkeypatch.delenv("ANN_PERSIST", raising=False)
+        nxt, _ = eng.prefill(prompt, temp, k, seed=5, step=0)
+        toks, lgs = [int(nxt[0])], []
+        for i in range(60):
+            nxt, lg = eng.decode(nxt, temp, k, seed=5, step=i + 1, want_logits=True)
+            toks.append(int(nxt[0]))
+            lgs.append(lg.cpu())
+        eng.check_device()
+        return toks, torch.stack(lgs)
+
+    ta, la = run(True, 0.0, 0)
+    tb, lb = run(False, 0.0, 0)
+    assert ta == tb
+    assert (la - lb).abs().max().item() < LOGIT_TOL
+    sa, _ = run(True, 0.9, 20)
+    sb, _ = run(False, 0.9, 20)
+    assert sa == sb
+
+
 def test_long_context_decode():
     """Decode at positions up to 2100 on a full-causal layer (the split count
     caps at 32, several 64-key chunks per split) and a windowed layer."""
