@@ -44,6 +44,20 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Sum over a whole wave in a fixed order with DPP row operations (device
+// library wavefront reduction); every lane gets the total.
+extern "C" __device__ float __ockl_wfred_add_f32(float);
+__device__ __forceinline__ float wave_sum(float v) { return __ockl_wfred_add_f32(v); }
+
+// Sum over each group of 4 consecutive lanes (DPP quad permutes).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1,
+                                                            0xf, 0xf, false));   // [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E,
+                                                            0xf, 0xf, false));   // [2,3,0,1]
+  return v;
+}
+
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll

@@ -61,23 +61,26 @@ __device__ __forceinline__ void ll_store(u64* p, uint32_t v, uint32_t tag) {
 __device__ __forceinline__ u64 ll_load(const u64* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Wait until the word carries `tag`; bounded (see the file comment).
+// Wait until the word carries `tag`; bounded (see the file comment).  Two
+// polls stay in flight, so a ready word is seen about one load latency after
+// it lands instead of up to two.
 __device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
-  u64 v = ll_load(p);
-  unsigned s = 0;
-  while ((uint32_t)(v >> 32) != tag) {
-    ++s;
-    if ((s & 127u) == 0) {
+  u64 a = ll_load(p);
+  for (unsigned s = 0;; s += 2) {
+    __builtin_amdgcn_s_sleep(1);
+    const u64 b = ll_load(p);
+    if ((uint32_t)(a >> 32) == tag) return (uint32_t)a;
+    if ((s & 127u) == 0 && s) {
       if (s >= PD_SPIN) {
         atomicOr(err, 1u);
-        break;
+        return (uint32_t)b;
       }
-      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return (uint32_t)b;
     }
     __builtin_amdgcn_s_sleep(1);
-    v = ll_load(p);
+    a = ll_load(p);
+    if ((uint32_t)(b >> 32) == tag) return (uint32_t)b;
   }
-  return (uint32_t)v;
 }
 // dst[i] = data of src[i] for i < n, all loads of a thread issued first.
 __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, uint32_t tag,
@@ -97,6 +100,10 @@ __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, ui
   }
 }
 
+// Rows per wave of the K = d projections held in registers (U = UD chunks
+// each); the K = 4d projection holds one row of 4 UD chunks.
+constexpr int pd_rows_per_wave(int ud) { return ud == 3 ? 3 : 2; }
+
 // Rows of a projection owned by work-group g: pairs [b, e) of npairs.
 __device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr) {
   const int g = blockIdx.x, G = gridDim.x;
@@ -105,12 +112,13 @@ __device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr) {
   nr = 2 * (e - b);
 }
 
-// Weight chunks of this lane: row n0 + wave + 8 rr, chunks lane + 64 u.
-template <int U>
+// Weight chunks of this lane: row n0 + wave + 8 rr (rr < R), chunks
+// lane + 64 u (u < U).
+template <int U, int R>
 __device__ __forceinline__ void pd_wload(const bf16_t* W, int K, int n0, int nr, uint4* wr) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
 #pragma unroll
-  for (int rr = 0; rr < PD_SLOTS / U; ++rr) {
+  for (int rr = 0; rr < R; ++rr) {
     const int r = wv + PD_NW * rr;
     const bool ok = r < nr;
     const uint4* row = (const uint4*)(W + (size_t)(n0 + (ok ? r : 0)) * K);
@@ -123,12 +131,12 @@ __device__ __forceinline__ void pd_wload(const bf16_t* W, int K, int n0, int nr,
 }
 
 // stage[b][r] = dot(row r, gin[b]) for the nr rows of this work-group.
-template <int U, int BM>
+template <int U, int R, int BM>
 __device__ __forceinline__ void pd_wdot(const uint4* wr, const uint4* gin, int K, int nr,
                                         float (*stage)[PD_RMAX]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
 #pragma unroll
-  for (int rr = 0; rr < PD_SLOTS / U; ++rr) {
+  for (int rr = 0; rr < R; ++rr) {
     const int r = wv + PD_NW * rr;
     if (r < nr) {
       float acc[BM];
@@ -144,7 +152,7 @@ __device__ __forceinline__ void pd_wdot(const uint4* wr, const uint4* gin, int K
       }
 #pragma unroll
       for (int b = 0; b < BM; ++b) {
-        const float t = group_sum<64>(acc[b]);
+        const float t = wave_sum(acc[b]);
         if (lane == 0) stage[b][r] = t;
       }
     }
@@ -169,7 +177,7 @@ __device__ __forceinline__ void pd_rms(const bf16_t* src, bf16_t* dst, int K, fl
       const float a = __uint_as_float(w << 16), c = __uint_as_float(w & 0xffff0000u);
       ss += a * a + c * c;
     }
-    ss = group_sum<64>(ss);
+    ss = wave_sum(ss);
     if (lane == 0) red[b][wv] = ss;
   }
   __syncthreads();
@@ -222,11 +230,10 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
 template <int DH, int BM, int UD>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int KU = DH / 32;       // K slices per lane per chunk (4 lanes per key)
-  constexpr int VL = DH / 8;        // lanes per V row
-  constexpr int VP = 64 / VL;       // V rows per pass
-  constexpr int VU = PD_KW / VP;    // V passes per chunk
+  constexpr int VD = DH / 64;       // output dims per lane in P.V
   constexpr int P2 = DH / 2, D4 = DH / 4;
   constexpr int PD_RING = DH == 128 ? 2 : 3;   // key chunks in flight per wave
+  constexpr int RD = pd_rows_per_wave(UD);      // rows per wave, K = d projections
 
   extern __shared__ uint4 lds4[];
   __shared__ float stage[BM][PD_RMAX];
@@ -274,13 +281,13 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
     // ---- 1: qkv
     pd_rows(3 * d2, n0, nr);
-    pd_wload<UD>(Wl + P.o_qkv, d, n0, nr, wr);
+    pd_wload<UD, RD>(Wl + P.o_qkv, d, n0, nr, wr);
     if (l > 0) {
       ll_poll(P.xx, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
       __syncthreads();
     }
     pd_rms<BM>(sxs, gin, d, P.eps, red);
-    pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+    pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
     pd_emit<PE_STORE, BM>(stage, n0, nr, P.xq, 3 * d2, t1, lam, nullptr, nullptr, d);
 
     // ---- 2: attention of (b, h, split)
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     const bool attn = g < BM * H * S;
     // o projection weights for phase 3: now on work-groups without attention,
     // after it on the others (keeps the K/V ring and these apart)
-    if (!attn) pd_wload<UD>(Wl + P.o_o, d, n0, nr, wr);
+    if (!attn) pd_wload<UD, RD>(Wl + P.o_o, d, n0, nr, wr);
     if (attn) {
       const int s = g % S, h = (g / S) % H, b = g / (S * H);
       const int p = s_pos[b];
@@ -305,10 +312,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       bf16_t* vcl = P.vc + P.kvl * l;
       const bf16_t* kh = kcl + ho;
       const bf16_t* vh = vcl + ho;
-      const int sk = lane >> 2, sd = (lane & 3) * (DH / 4);
-      const int vr = lane / VL, vd = (lane % VL) * 8;
+      const int sk = lane >> 2, sd = (lane & 3) * (DH / 4);   // score: key, first dim
       auto cbase = [&](int t) { return k0 + PD_KW * (wv + PD_NW * t); };
-      auto load = [&](int t, uint4* kr, uint4* vr4) {
+      // K: 4 lanes x Dh/4 dims per key; V: every key's VD dims of this lane
+      auto load = [&](int t, uint4* kr, uint32_t* vr) {
         const int c = cbase(t);
         const int j = c + sk;
         const bool ok = j < k1 && j != p;
@@ -316,16 +323,26 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         for (int u = 0; u < KU; ++u)
           kr[u] = ok ? *(const uint4*)(kh + (size_t)j * DH + sd + u * 8) : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int u = 0; u < VU; ++u) {
-          const int jj = c + vr + u * VP;
-          vr4[u] = (jj < k1 && jj != p) ? *(const uint4*)(vh + (size_t)jj * DH + vd)
-                                        : make_uint4(0u, 0u, 0u, 0u);
+        for (int u = 0; u < PD_KW; ++u) {
+          const int jj = c + u;
+          const bool okv = jj < k1 && jj != p;
+          if (VD == 2)
+            vr[u] = okv ? *(const uint32_t*)(vh + (size_t)jj * DH + 2 * lane) : 0u;
+          else
+            vr[u] = okv ? (uint32_t)vh[(size_t)jj * DH + lane] : 0u;
         }
       };
-      uint4 kb[PD_RING][KU], vb[PD_RING][VU];
+      uint4 kb[PD_RING][KU];
+      uint32_t vb[PD_RING][PD_KW];
 #pragma unroll
       for (int r = 0; r < PD_RING - 1; ++r)
         if (r < nt) load(r, kb[r], vb[r]);
+      // RoPE table entries of position p (independent of the wait below)
+      float rc = 0.f, rsn = 0.f;
+      if (tid < D4) {
+        rc = P.cs[(size_t)p * D4 + tid];
+        rsn = P.sn[(size_t)p * D4 + tid];
+      }
       // q, k, v of this head from phase 1
       const u64* src = P.xq + (size_t)b * 3 * d2 + h * P2;
       for (int i = tid; i < 3 * P2; i += PD_T) {
@@ -333,30 +350,34 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         s_in[i] = ll_wait(src + part * d2 + k, t1, P.err);
       }
       __syncthreads();
-      if (tid < P2) {   // QK-norm + RoPE, one dim pair per lane
-        const uint32_t qw = s_in[tid], kw = s_in[P2 + tid], vw = s_in[2 * P2 + tid];
+      if (tid < 64) {   // QK-norm + RoPE, one dim pair per lane (lanes >= Dh/2 idle)
+        const bool on = tid < P2;
+        const uint32_t qw = on ? s_in[tid] : 0u, kw = on ? s_in[P2 + tid] : 0u;
         float q0 = __uint_as_float(qw << 16), q1 = __uint_as_float(qw & 0xffff0000u);
         float c0 = __uint_as_float(kw << 16), c1 = __uint_as_float(kw & 0xffff0000u);
-        const float sq = group_sum<P2>(q0 * q0 + q1 * q1);
-        const float sk2 = group_sum<P2>(c0 * c0 + c1 * c1);
+        const float sq = wave_sum(q0 * q0 + q1 * q1);
+        const float sk2 = wave_sum(c0 * c0 + c1 * c1);
         const float rq = rsqrtf(sq / (float)DH + P.eps), rk = rsqrtf(sk2 / (float)DH + P.eps);
         q0 = rbf(q0 * rq); q1 = rbf(q1 * rq);
         c0 = rbf(c0 * rk); c1 = rbf(c1 * rk);
         if (tid < D4) {
-          const float c = P.cs[(size_t)p * D4 + tid], sn = P.sn[(size_t)p * D4 + tid];
+          const float c = rc, sn = rsn;
           const float a0 = c * q0 + sn * q1, a1 = c * q1 - sn * q0;
           const float b0 = c * c0 + sn * c1, b1 = c * c1 - sn * c0;
           q0 = a0; q1 = a1; c0 = b0; c1 = b1;
         }
-        s_qp[tid] = pack2(q0, q1);
-        const uint32_t kp = pack2(c0, c1);
-        s_kp[tid] = kp;
-        s_v[2 * tid] = __uint_as_float(vw << 16);
-        s_v[2 * tid + 1] = __uint_as_float(vw & 0xffff0000u);
-        if (k0 <= p && p < k1) {   // this split owns p: append to the cache
-          const size_t ci = ho + (size_t)p * DH + 2 * tid;
-          *(uint32_t*)(kcl + ci) = kp;
-          *(uint32_t*)(vcl + ci) = vw;
+        if (on) {
+          const uint32_t vw = s_in[2 * P2 + tid];
+          s_qp[tid] = pack2(q0, q1);
+          const uint32_t kp = pack2(c0, c1);
+          s_kp[tid] = kp;
+          s_v[2 * tid] = __uint_as_float(vw << 16);
+          s_v[2 * tid + 1] = __uint_as_float(vw & 0xffff0000u);
+          if (k0 <= p && p < k1) {   // this split owns p: append to the cache
+            const size_t ci = ho + (size_t)p * DH + 2 * tid;
+            *(uint32_t*)(kcl + ci) = kp;
+            *(uint32_t*)(vcl + ci) = vw;
+          }
         }
       }
       __syncthreads();
@@ -364,11 +385,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 #pragma unroll
       for (int e = 0; e < DH / 8; ++e) qp[e] = s_qp[sd / 2 + e];
       const float sl2 = P.scale * 1.4426950408889634f, sh2 = P.shift * 1.4426950408889634f;
-      float acc[8];
+      float acc[VD];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-      float lsum = 0.f;
-      auto compute = [&](int t, const uint4* kr, const uint4* vr4) {
+      for (int e = 0; e < VD; ++e) acc[e] = 0.f;
+      float lsum = 0.f;   // wave-uniform
+      auto compute = [&](int t, const uint4* kr, const uint32_t* vr) {
         const int c = cbase(t);
         const int j = c + sk;
         float sc = 0.f;
@@ -384,23 +405,24 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
             sc = pd_dot2(qp[4 * u + 3], kr[u].w, sc);
           }
         }
-        sc += __shfl_xor(sc, 1, 64);
-        sc += __shfl_xor(sc, 2, 64);
+        sc = quad_sum(sc);
         const float pj = j < k1 ? __builtin_amdgcn_exp2f(sc * sl2 - sh2) : 0.f;
-        if ((lane & 3) == 0) lsum += pj;
 #pragma unroll
-        for (int u = 0; u < VU; ++u) {
-          const int r = vr + u * VP;
-          const float pr = __shfl(pj, 4 * r, 64);
-          float vf[8];
-          if (c + r == p) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = s_v[vd + e];
+        for (int u = 0; u < PD_KW; ++u) {
+          const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * u));
+          lsum += pu;
+          float v0, v1 = 0.f;
+          if (c + u == p) {
+            v0 = s_v[VD * lane];
+            if (VD == 2) v1 = s_v[VD * lane + 1];
+          } else if (VD == 2) {
+            v0 = __uint_as_float(vr[u] << 16);
+            v1 = __uint_as_float(vr[u] & 0xffff0000u);
           } else {
-            unpack8(vr4[u], vf);
+            v0 = __uint_as_float(vr[u] << 16);
           }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += pr * vf[e];
+          acc[0] += pu * v0;
+          if (VD == 2) acc[VD - 1] += pu * v1;
         }
       };
       for (int t = 0; t < nt; t += PD_RING) {
@@ -414,14 +436,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         }
       }
 #pragma unroll
-      for (int o = VL; o < 64; o <<= 1)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
-      lsum = group_sum<64>(lsum);
-      if (lane < VL) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s_o[wv][vd + e] = acc[e];
-      }
+      for (int e = 0; e < VD; ++e) s_o[wv][VD * lane + e] = acc[e];
       if (lane == 0) s_l[wv] = lsum;
       __syncthreads();
       u64* dst = P.xp + (size_t)g * (DH + 1);   // g = (b * H + h) * S + s
@@ -437,7 +452,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         for (int w = 0; w < PD_NW; ++w) lt += s_l[w];
         ll_store(dst + DH, __float_as_uint(lt), t1 + 1u);
       }
-      pd_wload<UD>(Wl + P.o_o, d, n0, nr, wr);
+      pd_wload<UD, RD>(Wl + P.o_o, d, n0, nr, wr);
     }
 
     // ---- 3: o = combine(partials); x' = mix_attn(x, x0, o Wo^T)
@@ -456,25 +471,25 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         gin[i] = f2bf(o / lt);
       }
       __syncthreads();
-      pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+      pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
       pd_emit<PE_ATTN, BM>(stage, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d);
     }
 
     // ---- 4: h = relu2(rms(x') Wfc^T)
     pd_rows(2 * d, n0, nr);
-    pd_wload<UD>(Wl + P.o_fc, d, n0, nr, wr);
+    pd_wload<UD, RD>(Wl + P.o_fc, d, n0, nr, wr);
     ll_poll(P.xm, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
     __syncthreads();
     pd_rms<BM>(sxm, gin, d, P.eps, red);
-    pd_wdot<UD, BM>(wr, (const uint4*)gin, d, nr, stage);
+    pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
     pd_emit<PE_RELU2, BM>(stage, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr, nullptr, d);
 
     // ---- 5: x = mix_mlp(x', h Wproj^T)
     pd_rows(d2, n0, nr);
-    pd_wload<4 * UD>(Wl + P.o_proj, 4 * d, n0, nr, wr);
+    pd_wload<4 * UD, 1>(Wl + P.o_proj, 4 * d, n0, nr, wr);
     ll_poll(P.xh, BM * 2 * d, (uint32_t*)gin, t1 + 3u, P.err);
     __syncthreads();
-    pd_wdot<4 * UD, BM>(wr, (const uint4*)gin, 4 * d, nr, stage);
+    pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)gin, 4 * d, nr, stage);
     pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d);
   }
 
@@ -520,7 +535,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         }
 #pragma unroll
         for (int b = 0; b < BM; ++b) {
-          const float y = group_sum<64>(acc[b]);
+          const float y = wave_sum(acc[b]);
           const bf16_t zb = f2bf(y);
           if (P.greedy) {
             const u64 key = n < P.Vs ? (((u64)zkey(zb) << 16) | (u64)(0xffffu - (uint32_t)n)) : 0ull;
@@ -606,12 +621,9 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
   if (B != 1 || ud == 0 || (Dh != 64 && Dh != 128) || d % 16 || V % 2 || V > 65536 || L > 50 ||
       G < 1)
     return false;
-  const int d2 = d / 2;
+  const int d2 = d / 2, rd = PD_NW * pd_rows_per_wave(ud);
   auto rows = [&](int npairs) { return 2 * ((npairs + G - 1) / G); };
-  if (rows(3 * d2) > PD_NW * (PD_SLOTS / ud)) return false;
-  if (rows(d2) > PD_NW * (PD_SLOTS / ud)) return false;
-  if (rows(2 * d) > PD_NW * (PD_SLOTS / ud)) return false;
-  if (PD_SLOTS / (4 * ud) < 1 || rows(d2) > PD_NW * (PD_SLOTS / (4 * ud))) return false;
+  if (rows(3 * d2) > rd || rows(d2) > rd || rows(2 * d) > rd || rows(d2) > PD_NW) return false;
   if (B * H * s_long > G || s_long < 1) return false;
   return true;
 }

@@ -392,8 +392,11 @@ void drop_graph(ann_ctx* c) {
   c->graph = nullptr;
 }
 
-int pd_splits(const ann_ctx* c, int B) {
-  int s = (c->c.max_ctx + 383) / 384;
+// Splits per (b, h) of the persistent step's attention: about 128 keys per
+// work-group (one 16-key chunk per wave, issued before the wait for q/k/v).
+int pd_splits(const ann_ctx* c, int B, bool lng) {
+  const int keys = lng ? c->c.max_ctx : (c->c.window < c->c.max_ctx ? c->c.window : c->c.max_ctx);
+  int s = (keys + 127) / 128;
   if (s > PD_MAX_SLONG) s = PD_MAX_SLONG;
   if (c->n_cu > 0 && s > c->n_cu / (B * c->c.H)) s = c->n_cu / (B * c->c.H);
   return s < 1 ? 1 : s;
@@ -413,7 +416,7 @@ bool persist_ok(ann_ctx* c, int B) {
   }
   const ann_config& g = c->c;
   return c->n_cu > 0 && g.n_long <= 8 &&
-         decode_persist_fits(B, g.d, g.H, c->Dh, g.V, g.L, c->n_cu, pd_splits(c, B));
+         decode_persist_fits(B, g.d, g.H, c->Dh, g.V, g.L, c->n_cu, pd_splits(c, B, true));
 }
 
 int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
@@ -457,8 +460,8 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.Vs = g.V_sample;
   P.max_ctx = g.max_ctx;
   P.window = g.window;
-  P.s_win = 1;
-  P.s_long = pd_splits(c, B);
+  P.s_win = pd_splits(c, B, false);
+  P.s_long = pd_splits(c, B, true);
   P.greedy = greedy ? 1 : 0;
   P.scale = g.attn_scale;
   P.shift = g.attn_scale * (float)c->Dh * 1.02f;
