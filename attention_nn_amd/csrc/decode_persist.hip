@@ -1,6 +1,7 @@
 // Persistent decode step for batch 1: embed, every layer, lm_head and the
-// greedy argmax of one token in ONE cooperative launch of one 512-thread
-// work-group per CU (model.py:223-263 for T = 1, sample.py:44-49 greedy).
+// greedy argmax of one token in ONE launch of one 512-thread work-group per
+// CU, all resident at once (model.py:223-263 for T = 1, sample.py:44-49
+// greedy).
 //
 // Why: at batch 1 a decode step is ~57 dependent phases whose own work is a
 // few microseconds of weight streaming; as separate kernels every phase pays
@@ -27,7 +28,7 @@
 // Every wait is bounded: after PD_SPIN polls (or once any work-group has
 // flagged a timeout in *err) it gives up and the kernel runs to its end, so
 // all waves always exit; the host reports a set flag as an error.  The grid
-// must be co-resident (cooperative launch, one work-group per CU).
+// must be co-resident: one work-group per CU, a CU holds one (see pd_launch).
 #include <math.h>
 #include "common.h"
 #include "launch.h"
@@ -632,8 +633,14 @@ size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
   return (size_t)7 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
 }
 
+// Launch of the G work-groups.  The grid is one work-group per CU and a CU
+// holds one (occupancy checked), so once the stream's earlier work has
+// drained every work-group is resident; a plain launch is measured ~19 us per
+// step cheaper than a cooperative one (which the runtime serialises), and the
+// bounded waits end the kernel with the error flag set should residency ever
+// fail.  coop: use the cooperative launch instead.
 template <int DH, int BM, int UD>
-static hipError_t pd_launch(const PDParams& P, int G, size_t lds, hipStream_t st) {
+static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hipStream_t st) {
   const void* fn = (const void*)k_decode_persist<DH, BM, UD>;
   static bool attr = false;
   if (!attr) {
@@ -648,19 +655,20 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, hipStream_t st
   if (nb < 1) return hipErrorCooperativeLaunchTooLarge;
   PDParams a = P;
   void* args[] = {&a};
-  return hipLaunchCooperativeKernel(fn, dim3(G), dim3(PD_T), args, (unsigned)lds, st);
+  if (coop) return hipLaunchCooperativeKernel(fn, dim3(G), dim3(PD_T), args, (unsigned)lds, st);
+  return hipLaunchKernel(fn, dim3(G), dim3(PD_T), args, lds, st);
 }
 
-hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, hipStream_t st) {
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st) {
   const size_t lds = decode_persist_lds(B, P.d, P.H, Dh, P.s_long);
   if (lds > 144 * 1024 || B != 1) return hipErrorInvalidValue;
   switch (Dh * 16 + decode_persist_slots(P.d)) {
-    case 64 * 16 + 1: return pd_launch<64, 1, 1>(P, G, lds, st);
-    case 64 * 16 + 2: return pd_launch<64, 1, 2>(P, G, lds, st);
-    case 64 * 16 + 3: return pd_launch<64, 1, 3>(P, G, lds, st);
-    case 128 * 16 + 1: return pd_launch<128, 1, 1>(P, G, lds, st);
-    case 128 * 16 + 2: return pd_launch<128, 1, 2>(P, G, lds, st);
-    case 128 * 16 + 3: return pd_launch<128, 1, 3>(P, G, lds, st);
+    case 64 * 16 + 1: return pd_launch<64, 1, 1>(P, G, lds, coop, st);
+    case 64 * 16 + 2: return pd_launch<64, 1, 2>(P, G, lds, coop, st);
+    case 64 * 16 + 3: return pd_launch<64, 1, 3>(P, G, lds, coop, st);
+    case 128 * 16 + 1: return pd_launch<128, 1, 1>(P, G, lds, coop, st);
+    case 128 * 16 + 2: return pd_launch<128, 1, 2>(P, G, lds, coop, st);
+    case 128 * 16 + 3: return pd_launch<128, 1, 3>(P, G, lds, coop, st);
     default: return hipErrorInvalidValue;
   }
 }

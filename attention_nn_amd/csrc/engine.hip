@@ -181,6 +181,7 @@ struct ann_ctx {
   // persistent batch-1 decode step
   int n_cu = -1;         // CUs of the device (queried on first use)
   bool pd_env = true;    // ANN_PERSIST=0 disables
+  bool pd_coop = false;  // ANN_PERSIST_COOP=1: cooperative launch
   bool pd_clear = true;  // exchange area must be cleared before the next use
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
@@ -468,7 +469,7 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.eps = g.rms_eps;
   {
     ProfScope ps(c, ANN_PROF_STEP, st);
-    HIPCHK(decode_persist(P, B, c->Dh, c->n_cu, st));
+    HIPCHK(decode_persist(P, B, c->Dh, c->n_cu, c->pd_coop, st));
   }
   if (!greedy)
     HIPCHK(sample(c->sp<bf16_t>(c->sl.zb), g.V, B, g.V_sample, c->sp<SampParams>(c->sl.sp),
@@ -532,6 +533,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->use_graph = !(ge && ge[0] == '0');
   const char* pe = getenv("ANN_PERSIST");
   c->pd_env = !(pe && pe[0] == '0');
+  const char* pc = getenv("ANN_PERSIST_COOP");
+  c->pd_coop = pc && pc[0] == '1';
   *out = c;
   return ANN_OK;
 }

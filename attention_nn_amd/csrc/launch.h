@@ -108,9 +108,9 @@ hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float 
 hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st);
 hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st);
 
-// Persistent decode step (batch 1): one cooperative launch of G work-groups
-// runs embed, all layers, lm_head and (greedy) the argmax; see
-// decode_persist.hip.  Exchange words are 64-bit (tag << 32 | data).
+// Persistent decode step (batch 1): one launch of G work-groups (one per
+// CU, all resident) runs embed, all layers, lm_head and (greedy) the argmax;
+// see decode_persist.hip.  Exchange words are 64-bit (tag << 32 | data).
 typedef unsigned long long u64;
 struct PDParams {
   const bf16_t* emb;
@@ -142,7 +142,7 @@ struct PDParams {
 };
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
-hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, hipStream_t st);
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st);
 
 hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st);
 hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,

@@ -10,14 +10,16 @@ whole model for the batch.  K steps (default 992 = positions 32..1023) are
 timed with HIP events on the stream the kernels run on, after W warm-up steps
 and a fresh prefill.  value = decoded tokens / s.
 
-roofline: the dominant kernel of the step (the lm_head projection fused
-with the softcap, 2*d*V weight bytes per launch).  The timed pass replays
-the step as one HIP graph, where events cannot bracket a single kernel, so a
-second pass over the identical workload launches the step eagerly with a HIP
-event pair around every lm_head launch on the stream it runs on; achieved =
-algorithmic bytes per launch / mean launch time, against the 8 TB/s peak.
+roofline: the dominant kernel -- at batch 1 the whole decode step is one
+persistent kernel (k_decode_persist: embed, every layer, lm_head + softcap,
+greedy argmax in one cooperative launch).  The timed pass replays it from a
+HIP graph, where events cannot bracket it, so a second pass over the
+identical workload launches it eagerly with a HIP event pair around every
+launch on the stream it runs on; achieved = algorithmic bytes of the step
+(bf16 weights once, K/V rows read and appended, embedding row) / mean
+launch time, against the 8 TB/s peak.
 
-secondary: the whole decode step against the HBM roofline, batch-64 decode
+secondary: the step's wall rate, batch-64 decode
 (configs[2]: 512-token prompts, temperature 0.8, top-k 50) and its prefill
 against the bf16 MFMA peak.
 
@@ -70,16 +72,12 @@ def prefill_flops(cfg, B, T):
     return f
 
 
-def lm_head_bytes(cfg, B):
-    d, V = cfg.model_dim, cfg.vocab_size
-    return 2 * d * V + 2 * B * d + 2 * B * V
-
-
-def lm_head_traffic():
-    """HBM bytes per lm_head launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (scaled by a known-size copy), or None."""
+def step_traffic():
+    """HBM bytes per launch of the persistent decode kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a known-size copy),
+    or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "lm_head_b1_hbm_traffic.json")
+                        "decode_persist_b1_hbm_traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
@@ -88,7 +86,7 @@ def lm_head_traffic():
         return None
 
 
-def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=True):
+def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=None):
     import torch
     B = prompt.shape[0]
     if warmup:
@@ -99,7 +97,7 @@ def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=True):
     nxt, _ = eng.prefill(prompt, temperature, top_k, seed, 0)
     torch.cuda.synchronize()
     if prof:
-        eng.profile("lm_head", max_launches=steps + 8)
+        eng.profile(prof, max_launches=steps + 8)
     st = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -111,9 +109,9 @@ def run_decode(eng, prompt, steps, warmup, temperature, top_k, seed, prof=True):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1)
-    head = eng.profile_read() if prof else (0.0, 0)
+    kern = eng.profile_read() if prof else (0.0, 0)
     eng.profile(None)
-    return ms, wall, head, B * steps
+    return ms, wall, kern, B * steps
 
 
 def cpu_baseline(cfg, params, prompt_len, ctx_end, budget_s=20.0):
@@ -174,7 +172,7 @@ def secondary_b64(cfg, params):
     torch.cuda.synchronize()
     pms = e0.elapsed_time(e1) / reps
     pf = prefill_flops(cfg, B, P)
-    ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7, prof=False)
+    ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7)
     b64_bytes = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
     b64_gbs = b64_bytes / (ms64 / S / 1e3) / 1e9
     tf = pf / (pms / 1e3) / 1e12
@@ -214,7 +212,7 @@ def extra_config(name):
     e1.record()
     torch.cuda.synchronize()
     pms = e0.elapsed_time(e1)
-    ms, _, _, toks = run_decode(eng, pr, S, 0, temp, k, 11, prof=False)
+    ms, _, _, toks = run_decode(eng, pr, S, 0, temp, k, 11)
     byts = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
     gbs = byts / (ms / S / 1e3) / 1e9
     pf = prefill_flops(cfg, B, P)
@@ -238,6 +236,9 @@ def main():
                     help="run only the batch-64 prefill/decode section (for profiling)")
     ap.add_argument("--configs", type=str, default="",
                     help="comma list of extra workloads to add as secondary lines: cfg4,cfg5")
+    ap.add_argument("--trace-run", action="store_true",
+                    help="run only the batch-1 workload (prefill + K graph-replayed decode "
+                         "steps, no event instrumentation) for rocprofv3 traces and counters")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 512 MiB device-to-device (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -269,16 +270,25 @@ def main():
         print(json.dumps(secondary_b64(cfg, params)), flush=True)
         return 0
     eng = Engine(cfg, params, max_batch=1, max_ctx=1024, max_tokens=1024)
-    # timed pass: the decode step replays as one captured HIP graph
-    ms, wall, _, toks = run_decode(eng, prompt, steps, args.warmup, 0.0, 0, 0, prof=False)
-    # roofline pass: same workload launched eagerly with a HIP event pair
-    # around every lm_head launch (events cannot sit inside the replayed graph)
-    _, _, (head_ms, head_n), _ = run_decode(eng, prompt, steps, 0, 0.0, 0, 0, prof=True)
+    if args.trace_run:
+        nxt, _ = eng.prefill(prompt, 0.0, 0, 0, 0)
+        for i in range(steps):
+            nxt, _ = eng.decode(nxt, 0.0, 0, 0, i + 1, out=nxt)
+        torch.cuda.synchronize()
+        eng.check_device()
+        print(f"trace run: prefill {prompt_len} + {steps} greedy decode steps", flush=True)
+        return 0
+    # timed pass: the decode step replays as one captured HIP graph (one
+    # cooperative launch of the persistent step kernel per token)
+    ms, wall, _, toks = run_decode(eng, prompt, steps, args.warmup, 0.0, 0, 0)
+    # roofline pass: same workload launched eagerly with a HIP event pair on
+    # the call's stream around every launch of the step kernel (events cannot
+    # sit inside the replayed graph)
+    _, _, (k_ms, k_n), _ = run_decode(eng, prompt, steps, 0, 0.0, 0, 0, prof="step")
     value = toks / (ms / 1e3)
     avg_bytes = np.mean([step_bytes(cfg, 1, prompt_len + i) for i in range(steps)])
-    head_avg_ms = head_ms / max(head_n, 1)
-    head_b = lm_head_bytes(cfg, 1)
-    achieved = head_b / (head_avg_ms / 1e3) / 1e9
+    k_avg_ms = k_ms / max(k_n, 1)
+    achieved = avg_bytes / (k_avg_ms / 1e3) / 1e9
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -297,11 +307,13 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": lm_head_traffic(),
-                     "traffic_source": "profiles/lm_head_b1_hbm_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
-                     "kernel": "k_gemv<1,32,EPI_LOGITS,rms> (lm_head + softcap)",
-                     "bytes_per_launch": head_b, "avg_launch_us": round(head_avg_ms * 1e3, 3),
-                     "launches": head_n},
+                     "traffic": step_traffic(),
+                     "traffic_source": "profiles/decode_persist_b1_hbm_traffic.md (rocprofv3 "
+                                       "FETCH_SIZE/WRITE_SIZE)",
+                     "kernel": "k_decode_persist<128,1,2> (whole batch-1 decode step: embed, 11 "
+                               "layers, lm_head + softcap, greedy argmax)",
+                     "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(k_avg_ms * 1e3, 3),
+                     "launches": k_n},
     }
     step_gbs = avg_bytes / (ms / steps / 1e3) / 1e9
     sec = {"b1_step": {"avg_alg_bytes": int(avg_bytes), "achieved_GBs": round(step_gbs, 1),

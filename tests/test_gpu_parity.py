@@ -163,6 +163,29 @@ def test_persistent_decode_matches_oracle(name):
     assert worst < LOGIT_TOL, worst
 
 
+def test_persistent_cooperative_launch(monkeypatch):
+    """ANN_PERSIST_COOP=1 launches the same step kernel cooperatively (the
+    runtime guarantees residency); logits still match the oracle."""
+    monkeypatch.setenv("ANN_PERSIST_COOP", "1")
+    cfg = small_cfgs()["dh64"]
+    p = perturb_lambdas(init_params(cfg, 16, dense=True))
+    tok = np.random.default_rng(13).integers(0, cfg.vocab_size, (1, 30))
+    eng = _engine(cfg, p, 1)
+    monkeypatch.delenv("ANN_PERSIST_COOP")
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :5], want_logits=True)
+    R.forward(prep, tok[:, :5], cache)
+    worst = 0.0
+    for i in range(5, 29):
+        t = tok[:, i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
+    assert worst < LOGIT_TOL, worst
+
+
 def test_persistent_matches_kernel_path(monkeypatch):
     """The persistent batch-1 step and the per-kernel step (ANN_PERSIST=0)
     agree: greedy tokens identical over 60 steps and logits within the oracle
