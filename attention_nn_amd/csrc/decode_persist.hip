@@ -64,11 +64,10 @@ __device__ __forceinline__ u64 ll_load(const u64* p) {
 }
 // Wait until the word carries `tag`; bounded (see the file comment).  Two
 // polls stay in flight, so a ready word is seen about one load latency after
-// it lands instead of up to two.
+// it lands instead of up to two; no sleep between them (measured faster).
 __device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
   u64 a = ll_load(p);
   for (unsigned s = 0;; s += 2) {
-    __builtin_amdgcn_s_sleep(1);
     const u64 b = ll_load(p);
     if ((uint32_t)(a >> 32) == tag) return (uint32_t)a;
     if ((s & 127u) == 0 && s) {
@@ -78,7 +77,6 @@ __device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* e
       }
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return (uint32_t)b;
     }
-    __builtin_amdgcn_s_sleep(1);
     a = ll_load(p);
     if ((uint32_t)(b >> 32) == tag) return (uint32_t)b;
   }
