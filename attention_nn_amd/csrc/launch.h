@@ -63,7 +63,7 @@ bool gemv_fits(int M, int K);
 int gemv_blocks(int N, int K);
 hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
                            int32_t* pos, int pos_adv, hipStream_t st);
-// Skinny MFMA GEMM for decode (M <= 64, K % 128 == 0): y = pre(A) @ W^T,
+// Skinny MFMA GEMM for decode (M <= 128, K % 128 == 0): y = pre(A) @ W^T,
 // rms: A rows RMS-normalised in the kernel (K <= 3072).
 bool gemm_skinny_fits(int M, int N, int K, bool rms);
 hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,

@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
     }
 }
 
-// ---- skinny MFMA GEMM (decode, M <= 64) -------------------------------------
+// ---- skinny MFMA GEMM (decode, M <= 128) ------------------------------------
 //
 // One 16 (M) x 16 (N) output tile per work-group; the four waves split K into
 // quarters and each loads its whole quarter of A and W fragments (up to 24
@@ -387,104 +387,157 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
 
 constexpr int SK_KB = 24;   // largest batch of k-steps per wave
 
-template <int EPI, bool RMS, int KB>
+template <int EPI, bool RMS, int KB, int T>
 __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, int lda,
                                                  const bf16_t* __restrict__ W, int M, int N, int K,
                                                  float eps, EpiArgs ea) {
-  __shared__ floatx4_t red[3 * 64];
-  __shared__ float s_ss[4][16];
+  // work-group tile (16 T) x (16 T): T x T blocks of 16x16 per wave
+  __shared__ floatx4_t red[3][T * T][64];
+  __shared__ float s_ss[4][16 * T];
   const int tid = threadIdx.x, lane = tid & 63, wk = tid >> 6;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16 * T;
   const int kw = K >> 7;   // k-steps per wave
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  const int arow = m0 + r16, wrow = n0 + r16;
-  const bool aok = arow < M, wok = wrow < N;
-  const bf16_t* ap = A + (size_t)(aok ? arow : 0) * lda + wk * kw * 32 + kq;
-  const bf16_t* wp = W + (size_t)(wok ? wrow : 0) * K + wk * kw * 32 + kq;
-  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const bf16_t* ap[T];
+  const bf16_t* wp[T];
+  bool aok[T], wok[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int arow = m0 + 16 * t + r16, wrow = n0 + 16 * t + r16;
+    aok[t] = arow < M;
+    wok[t] = wrow < N;
+    ap[t] = A + (size_t)(aok[t] ? arow : 0) * lda + wk * kw * 32 + kq;
+    wp[t] = W + (size_t)(wok[t] ? wrow : 0) * K + wk * kw * 32 + kq;
+  }
+  floatx4_t acc[T][T];
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < kw; s0 += KB) {
-    uint4 ca[KB], cw[KB];
+    uint4 ca[KB][T], cw[KB][T];
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const bool ok = s0 + i < kw;
-      ca[i] = (ok && aok) ? *(const uint4*)(ap + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
-      cw[i] = (ok && wok) ? *(const uint4*)(wp + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
-    }
-    float scale = 1.f;
-    if (RMS) {   // the host guarantees kw <= KB: one pass, uniform barrier
-      float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < KB; ++i) {
-        float f[8];
-        unpack8(ca[i], f);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+      for (int t = 0; t < T; ++t) {
+        ca[i][t] = (ok && aok[t]) ? *(const uint4*)(ap[t] + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
+        cw[i][t] = (ok && wok[t]) ? *(const uint4*)(wp[t] + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
       }
-      ss += __shfl_xor(ss, 16, 64);
-      ss += __shfl_xor(ss, 32, 64);
-      if (lane < 16) s_ss[wk][lane] = ss;
+    }
+    float scale[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) scale[t] = 1.f;
+    if (RMS) {   // the host guarantees kw <= KB: one pass, uniform barrier
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          float f[8];
+          unpack8(ca[i][t], f);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (lane < 16) s_ss[wk][16 * t + lane] = ss;
+      }
       __syncthreads();
-      const float t = ((s_ss[0][r16] + s_ss[1][r16]) + s_ss[2][r16]) + s_ss[3][r16];
-      scale = rsqrtf(t / (float)K + eps);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int r = 16 * t + r16;
+        const float tt = ((s_ss[0][r] + s_ss[1][r]) + s_ss[2][r]) + s_ss[3][r];
+        scale[t] = rsqrtf(tt / (float)K + eps);
+      }
     }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       if (s0 + i < kw) {
-        uint4 a = ca[i];
-        if (RMS) {
-          float f[8];
-          unpack8(a, f);
-          a.x = pack2(f[0] * scale, f[1] * scale);
-          a.y = pack2(f[2] * scale, f[3] * scale);
-          a.z = pack2(f[4] * scale, f[5] * scale);
-          a.w = pack2(f[6] * scale, f[7] * scale);
+        uint4 a[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          a[t] = ca[i][t];
+          if (RMS) {
+            float f[8];
+            unpack8(a[t], f);
+            a[t].x = pack2(f[0] * scale[t], f[1] * scale[t]);
+            a[t].y = pack2(f[2] * scale[t], f[3] * scale[t]);
+            a[t].z = pack2(f[4] * scale[t], f[5] * scale[t]);
+            a[t].w = pack2(f[6] * scale[t], f[7] * scale[t]);
+          }
         }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(bf16x8_t*)&a, *(bf16x8_t*)&cw[i], acc, 0,
-                                                      0, 0);
+#pragma unroll
+        for (int ta = 0; ta < T; ++ta)
+#pragma unroll
+          for (int tw = 0; tw < T; ++tw)
+            acc[ta][tw] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                *(bf16x8_t*)&a[ta], *(bf16x8_t*)&cw[i][tw], acc[ta][tw], 0, 0, 0);
       }
     }
   }
-  if (wk > 0) red[(wk - 1) * 64 + lane] = acc;
+  if (wk > 0) {
+#pragma unroll
+    for (int ta = 0; ta < T; ++ta)
+#pragma unroll
+      for (int tw = 0; tw < T; ++tw) red[wk - 1][ta * T + tw][lane] = acc[ta][tw];
+  }
   __syncthreads();
   if (wk > 0) return;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const floatx4_t p = red[j * 64 + lane];
-    acc[0] += p[0];
-    acc[1] += p[1];
-    acc[2] += p[2];
-    acc[3] += p[3];
-  }
-  const int n = n0 + r16;
+  for (int ta = 0; ta < T; ++ta)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = m0 + (lane >> 4) * 4 + r;
-    if (m < M && n < N) epilogue<EPI>(ea, m, n, acc[r]);
-  }
+    for (int tw = 0; tw < T; ++tw) {
+      floatx4_t v = acc[ta][tw];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const floatx4_t p = red[j][ta * T + tw][lane];
+        v[0] += p[0];
+        v[1] += p[1];
+        v[2] += p[2];
+        v[3] += p[3];
+      }
+      const int n = n0 + 16 * tw + r16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * ta + (lane >> 4) * 4 + r;
+        if (m < M && n < N) epilogue<EPI>(ea, m, n, v[r]);
+      }
+    }
 }
 
 bool gemm_skinny_fits(int M, int N, int K, bool rms) {
-  return M > 0 && M <= 64 && N > 0 && K % 128 == 0 && (!rms || K / 128 <= SK_KB);
+  return M > 0 && M <= 128 && N > 0 && K % 128 == 0 &&
+         (!rms || K / 128 <= (M > 32 ? 12 : SK_KB));
 }
 
 hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
                        int K, float eps, const EpiArgs& ea, hipStream_t st) {
   if (!gemm_skinny_fits(M, N, K, rms) || lda % 8) return hipErrorInvalidValue;
-  dim3 grid((N + 15) / 16, (M + 15) / 16);
+  // 32x32 work-group tiles halve the L2 re-reads of A and W; 16x16 tiles give
+  // more work-groups.  Measured: 32x32 wins above 64 rows and for wide N at
+  // 33-64 rows, 16x16 for narrow N at 64 rows.
+  const int T = (M > 64 || (M > 32 && N >= 2048)) ? 2 : 1;
+  dim3 grid((N + 16 * T - 1) / (16 * T), (M + 16 * T - 1) / (16 * T));
   // batch depth: the wave's whole K quarter when it fits (fewer registers ->
   // more resident work-groups)
   const int kw = K >> 7;
   const int kb = kw <= 6 ? 6 : kw <= 12 ? 12 : SK_KB;
-#define ANN_SK_KB(E, R)                                                                      \
-  if (kb == 6)                                                                               \
-    hipLaunchKernelGGL((k_gemm_sk<E, R, 6>), grid, dim3(256), 0, st, A, lda, W, M, N, K, eps, \
-                       ea);                                                                  \
-  else if (kb == 12)                                                                         \
-    hipLaunchKernelGGL((k_gemm_sk<E, R, 12>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
-                       eps, ea);                                                             \
-  else                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk<E, R, SK_KB>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
-                       eps, ea);
+#define ANN_SK_T(E, R, KBV)                                                                   \
+  if (T == 1)                                                                                 \
+    hipLaunchKernelGGL((k_gemm_sk<E, R, KBV, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
+                       eps, ea);                                                              \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_gemm_sk<E, R, (KBV > 12 ? 12 : KBV), 2>), grid, dim3(256), 0, st, A, \
+                       lda, W, M, N, K, eps, ea);
+#define ANN_SK_KB(E, R)    \
+  if (kb == 6) {           \
+    ANN_SK_T(E, R, 6)      \
+  } else if (kb == 12) {   \
+    ANN_SK_T(E, R, 12)     \
+  } else {                 \
+    ANN_SK_T(E, R, SK_KB)  \
+  }
 #define ANN_SK(E)            \
   if (rms) {                 \
     ANN_SK_KB(E, true)       \
@@ -501,6 +554,7 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
     default: return hipErrorInvalidValue;
   }
 #undef ANN_SK_KB
+#undef ANN_SK_T
 #undef ANN_SK
   return hipGetLastError();
 }
