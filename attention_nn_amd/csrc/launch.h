@@ -75,13 +75,6 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
 hipError_t rms_apply(const bf16_t* x, int ldx, bf16_t* h, int ldh, int M, int d, float eps,
                      hipStream_t st);
 
-// Attention of M query rows (row m = token t = m % T of sequence b = m / T at
-// position pos[b] + t) against the KV cache.  nsplit > 1 splits each row's key
-// range over work-groups (flash-decoding) and merges them in a second kernel.
-hipError_t attention(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const int32_t* pos,
-                     bf16_t* out, float* part, int M, int T, int H, int Dh, int max_ctx,
-                     int window, bool long_layer, float scale, int nsplit, hipStream_t st);
-
 // Prefill attention (MFMA flash attention) of B x T query rows at positions
 // pos[b] + t against keys [window start, own position] of the cache.
 hipError_t attn_prefill(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, const int32_t* pos,
