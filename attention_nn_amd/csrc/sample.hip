@@ -75,19 +75,14 @@ __device__ uint32_t philox_x(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
   return c0;
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
-    const uint64_t w = ((uint64_t)hi << 32) | lo;
-    v = w > v ? w : v;
-  }
-  return v;
-}
+// Wave reductions of the device library (fixed-order DPP row operations).
+extern "C" __device__ unsigned long __ockl_wfred_max_u64(unsigned long);
+extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
+extern "C" __device__ unsigned __ockl_wfred_min_u32(unsigned);
+extern "C" __device__ int __ockl_wfred_add_i32(int);
 
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
-  v = wave_max_u64(v);
+  v = __ockl_wfred_max_u64(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
@@ -98,12 +93,10 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   return b;
 }
 
-// Block sum of per-thread counts; buf alternates between calls so that one
-// barrier per call suffices.
-__device__ __forceinline__ uint32_t block_count(uint32_t c, uint32_t* buf) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-  if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = c;
+// Block sum of per-wave counts (wc uniform within each wave); buf alternates
+// between calls so that one barrier per call suffices.
+__device__ __forceinline__ uint32_t block_sum_waves(uint32_t wc, uint32_t* buf) {
+  if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = wc;
   __syncthreads();
   uint32_t t = 0;
 #pragma unroll
@@ -118,6 +111,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
                                                         int32_t* __restrict__ pos, int pos_adv) {
   __shared__ uint32_t s_cnt[2][SMP_THREADS / 64];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
+  __shared__ uint32_t s_mm[2][SMP_THREADS / 64];
   __shared__ float s_wsum[SMP_THREADS / 64];
   __shared__ uint32_t s_misc[2];
   const float temperature = sp->temperature;
@@ -164,7 +158,24 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     }
     return;
   }
-  const uint32_t kmax = (uint32_t)block_max_u64(lmax, s_red);
+  // maximum key, and the smallest per-thread maximum over threads holding
+  // entries (a lower bound of the k-th largest key when top_k <= those threads)
+  {
+    const uint32_t wmax = __ockl_wfred_max_u32(lmax);
+    const uint32_t wmin = __ockl_wfred_min_u32(nvalid > 0 ? lmax : 0xffffffffu);
+    if (lane == 0) {
+      s_mm[0][wv] = wmax;
+      s_mm[1][wv] = wmin;
+    }
+  }
+  __syncthreads();
+  uint32_t kmax = 0, lmin = 0xffffffffu;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) {
+    kmax = s_mm[0][w] > kmax ? s_mm[0][w] : kmax;
+    lmin = s_mm[1][w] < lmin ? s_mm[1][w] : lmin;
+  }
+  const int holders = (Vs + SMP_PER - 1) / SMP_PER;   // threads with entries
 
   // ---- k-th largest key: largest T with count(key >= T) >= top_k
   uint32_t thr_key = 0;
@@ -172,14 +183,14 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   if (use_thr) {
     uint32_t lo = 0, hi = kmax;
     int round = 0;
-    if (top_k <= SMP_THREADS) {
+    if (top_k <= holders) {
       // lower bound: the top_k-th largest per-thread maximum (top_k threads
-      // each hold a key >= it)
-      uint32_t a = 0, b = kmax;
+      // each hold a key >= it), searched above the smallest maximum
+      uint32_t a = lmin, b = kmax;
       while (a < b) {
         const uint32_t mid = (a + b + 1) >> 1;
         const uint32_t c = (uint32_t)__popcll(__ballot(lmax >= mid));
-        const uint32_t tot = block_count(lane == 0 ? c : 0u, s_cnt[round++ & 1]);
+        const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
         if (tot >= (uint32_t)top_k) a = mid;
         else b = mid - 1;
       }
@@ -187,7 +198,8 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     }
     while (lo < hi) {
       const uint32_t mid = (lo + hi + 1) >> 1;
-      const uint32_t tot = block_count(count_ge(kk, mid), s_cnt[round++ & 1]);
+      const uint32_t c = (uint32_t)__ockl_wfred_add_i32((int)count_ge(kk, mid));
+      const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
       if (tot >= (uint32_t)top_k) lo = mid;
       else hi = mid - 1;
     }
