@@ -93,6 +93,8 @@ def test_call_order_and_capacity_errors(L):
         tok = ctypes.c_void_p(0x1000)
         # not bound yet
         assert L.ann_prefill(ctx, tok, 1, 4, ctypes.byref(s), tok, None, None) == _lib.ANN_E_STATE
+        assert L.ann_check_device(ctx, None) == _lib.ANN_E_STATE
+        assert L.ann_check_device(None, None) == _lib.ANN_E_ARG
         # bind with fake (never dereferenced) aligned pointers; sizes checked first
         wb = L.ann_weight_bytes(ctypes.byref(c))
         kb = L.ann_kv_bytes(ctypes.byref(c))
