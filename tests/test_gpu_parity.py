@@ -221,6 +221,45 @@ def test_persistent_matches_kernel_path(monkeypatch):
         assert sa[i + 1] == _sample_small(z, temp, k, S.uniform(5, i + 1, 0)), i
 
 
+@pytest.mark.parametrize("B", [40, 80])
+def test_decode_wide_batch_skinny_tiles(B):
+    """Decode at 40 and 80 rows: the skinny MFMA GEMM with 32x32 work-group
+    tiles (above 64 rows, and for N >= 2048 above 32 rows) against the oracle."""
+    cfg = GPTConfig(vocab_size=600, num_layers=2, num_heads=4, model_dim=512, seq_len=32,
+                    window=8, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 41, dense=True))
+    tok = np.random.default_rng(42).integers(0, cfg.vocab_size, (B, 12))
+    eng = _engine(cfg, p, B)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :9], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :9], cache)[:, -1]).abs().max().item()
+    for i in range(9, 11):
+        t = tok[:, i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    assert worst < LOGIT_TOL, worst
+
+
+def test_wide_lm_head_64_row_tile():
+    """A vocabulary wider than 8 d at 12 rows takes the large-tile MFMA GEMM
+    with its 64-row work-group tile for the lm_head."""
+    cfg = GPTConfig(vocab_size=4096, num_layers=1, num_heads=2, model_dim=128, seq_len=32,
+                    window=8, long_layers=(0,))
+    p = perturb_lambdas(init_params(cfg, 43, dense=True))
+    tok = np.random.default_rng(44).integers(0, cfg.vocab_size, (12, 6))
+    eng = _engine(cfg, p, 12)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :5], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :5], cache)[:, -1]).abs().max().item()
+    t = tok[:, 5]
+    _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+    worst = max(worst, (lg.cpu() - R.forward(prep, t[:, None], cache)[:, -1]).abs().max().item())
+    assert worst < LOGIT_TOL, worst
+
+
 def test_long_context_decode():
     """Decode at positions up to 2100 on a full-causal layer (the split count
     caps at 32, several 64-key chunks per split) and a windowed layer."""
