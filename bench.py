@@ -25,7 +25,7 @@ against the bf16 MFMA peak.
 
 cpu_baseline: the CPU oracle (PyTorch restatement of model.py's forward)
 with sample.py's semantics -- a full forward over the whole context for every
-token -- timed at 8 context lengths spanning 32..1023 and integrated over the
+token -- timed best-of-3 at 24 context lengths spanning 32..1023 and integrated over the
 loop; threads = the host cores this process may use.
 """
 
@@ -128,7 +128,7 @@ def cpu_baseline(cfg, params, prompt_len, ctx_end, budget_s=20.0):
     for T in ctxs:
         tok = rng.integers(0, 50257, (1, int(T)))
         best = None
-        for _ in range(2):
+        for _ in range(3):
             t0 = time.perf_counter()
             with torch.no_grad():
                 R.forward(prep, tok)
@@ -147,7 +147,7 @@ def cpu_baseline(cfg, params, prompt_len, ctx_end, budget_s=20.0):
         "unit": "tok/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle full-recompute forward (sample.py semantics, no KV cache), best of 2 "
+        "sample": (f"oracle full-recompute forward (sample.py semantics, no KV cache), best of 3 "
                    f"at {len(ctxs)} contexts {int(ctxs[0])}..{int(ctxs[-1])}, interpolated and "
                    f"summed over the {len(all_ctx)} steps {prompt_len}..{ctx_end - 1} "
                    f"({time.perf_counter() - t_start:.1f} s of CPU work)"),
