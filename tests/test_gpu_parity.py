@@ -116,6 +116,24 @@ def test_forward_logits_parity(name, B, T):
     assert torch.all((got > 0) & (got < 23))
 
 
+@pytest.mark.parametrize("dh,window", [(64, 70), (128, 100)])
+def test_prefill_logits_every_position_long_prompt(dh, window):
+    """Prefill of 300 tokens (three 128-query blocks, 64-key tiles): logits at
+    every position match the oracle.  The windows are not multiples of the key
+    tile, so the prefill attention meets tiles it evaluates unmasked, tiles
+    crossing the diagonal or the window edge, and tiles a wave skips."""
+    cfg = GPTConfig(vocab_size=700, num_layers=2, num_heads=2, model_dim=2 * dh, seq_len=320,
+                    window=window, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 23, dense=True))
+    tok = np.random.default_rng(dh + window).integers(0, cfg.vocab_size, (2, 300))
+    print(f"case dh={dh} window={window} B=2 T=300", flush=True)
+    eng = _engine(cfg, p, 2)
+    got = eng.forward_logits(tok).cpu()
+    ref = R.logits(cfg, p, tok)
+    err = (got - ref).abs().max().item()
+    assert err < LOGIT_TOL, err
+
+
 @pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 12)])
 def test_decode_teacher_forced_past_window(name, B):
     """Decode logits at every position (well past the window) match the
