@@ -221,12 +221,18 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
 };
 
 // y = pre(X) @ W^T for M rows with the given epilogue.
+// Whether proj() routes an (M, N, K) projection to the large-tile MFMA GEMM.
+bool proj_is_gemm(int M, int N, int K, int pre) {
+  // the skinny GEMM re-reads W per 16 rows and A per 16 columns: wide
+  // outputs (lm_head) go to the large-tile GEMM
+  return !gemv_fits(M, K) && !(N <= 8 * K && gemm_skinny_fits(M, N, K, pre == PRE_RMS));
+}
+
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st) {
   const bool use_gemv = gemv_fits(M, K);
-  // the skinny GEMM re-reads W per 16 rows and A per 16 columns: wide
-  // outputs (lm_head) go to the large-tile GEMM
-  const bool use_sk = !use_gemv && N <= 8 * K && gemm_skinny_fits(M, N, K, pre == PRE_RMS);
+  const bool use_sk = !use_gemv && !proj_is_gemm(M, N, K, pre);
+  if (epi == EPI_QKV && (use_gemv || use_sk)) return fail(ANN_E_ARG, "fused QKV needs the MFMA GEMM");
   if (pre == PRE_RMS && !use_gemv && !use_sk) {   // large GEMM: A normalised once into h
     if (K > c->c.d) return fail(ANN_E_ARG, "RMS prologue wider than the model dim");
     bf16_t* h = c->sp<bf16_t>(c->sl.hn);
@@ -280,8 +286,30 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
     EpiArgs ea{};
     ea.out = qkv;
     ea.ldo = 3 * d;
-    int rc = proj(c, ANN_PROF_QKV, EPI_STORE, PRE_RMS, c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d,
-                  ea, st);
+    // prefill on the MFMA GEMM: QK-norm, RoPE and the cache append run in the
+    // projection's epilogue (q lands in its own buffer, qkv is not written)
+    ea.kc = c->kcache(l);
+    ea.vc = c->vcache(l);
+    ea.pos = pos;
+    ea.cs = cs;
+    ea.sn = sn;
+    ea.T = T;
+    ea.H = H;
+    ea.Dh = Dh;
+    ea.max_ctx = g.max_ctx;
+    ea.eps = g.rms_eps;
+    bool fuse_qkv = false;
+    if (T > 1 && proj_is_gemm(M, 3 * d, d, PRE_RMS)) {
+      EpiArgs fq = ea;
+      fq.out = q;
+      fq.ldo = d;
+      if (gemm_qkv_fits(M, 3 * d, d, fq)) {
+        ea = fq;
+        fuse_qkv = true;
+      }
+    }
+    int rc = proj(c, ANN_PROF_QKV, fuse_qkv ? EPI_QKV : EPI_STORE, PRE_RMS,
+                  c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d, ea, st);
     if (rc) return rc;
     EpiArgs er{};
     er.x = x;
@@ -300,8 +328,9 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
                 er, st);
       if (rc) return rc;
     } else {
-      HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,
-                      g.rms_eps, st));
+      if (!fuse_qkv)
+        HIPCHK(qkv_post(qkv, q, c->kcache(l), c->vcache(l), pos, cs, sn, M, T, H, Dh, g.max_ctx,
+                        g.rms_eps, st));
       {
         ProfScope ps(c, ANN_PROF_ATTN, st);
         HIPCHK(attn_prefill(q, c->kcache(l), c->vcache(l), pos, ao, B, T, H, Dh, g.max_ctx,

@@ -13,7 +13,12 @@ namespace ann {
 //                   rounded to bf16                               (model.py:255-256)
 //   EPI_RESID_MLP   x = (r1*x) + (p1*bf16(y)), each op rounded     (model.py:259-260)
 //   EPI_LOGITS      z = bf16(y) -> zbuf (if set); softcap(z) -> logits fp32 (if set)
-enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4 };
+//   EPI_QKV         (MFMA GEMM only, prefill QKV projection) per head:
+//                   q = rope(rms(bf16(y_q))) -> out (M, ldo); k = rope(rms(bf16(y_k)))
+//                   and v = bf16(y_v) -> the KV cache at [b][h][pos[b] + t]
+//                   (model.py:244-247, 252)
+enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4,
+       EPI_QKV = 5 };
 
 struct EpiArgs {
   bf16_t* out;       // STORE / RELU2 output (M, ldo)
@@ -30,6 +35,14 @@ struct EpiArgs {
   // amax[m * blocks + block]; argmax_finalize turns them into tokens.
   unsigned long long* amax;
   int Vs;
+  // QKV: row m = b * T + t; model dim d = H * Dh; caches [B][H][max_ctx][Dh]
+  bf16_t* kc;
+  bf16_t* vc;
+  const int32_t* pos;
+  const float* cs;   // RoPE cos / sin tables (max_ctx, Dh / 4)
+  const float* sn;
+  int T, H, Dh, max_ctx;
+  float eps;
 };
 
 // Sampling parameters read by the sampler from device memory (so a captured
@@ -66,6 +79,7 @@ hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int
 // Skinny MFMA GEMM for decode (M <= 128, K % 128 == 0): y = pre(A) @ W^T,
 // rms: A rows RMS-normalised in the kernel (K <= 3072).
 bool gemm_skinny_fits(int M, int N, int K, bool rms);
+bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea);
 hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
                        int K, float eps, const EpiArgs& ea, hipStream_t st);
 // MFMA GEMM (prefill): y = A @ W^T with A (M, lda) bf16.

@@ -36,6 +36,63 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
   }
 }
 
+// Epilogue for the four consecutive columns n..n+3 of row m: one 8-byte
+// access per operand (16 bytes for fp32 logits) when all four columns exist
+// and the strides and bases keep the accesses aligned, else per element.
+template <int EPI>
+__device__ __forceinline__ bool epi_vec_ok(const EpiArgs& ea) {
+  if (EPI == EPI_STORE || EPI == EPI_RELU2)
+    return (ea.ldo & 3) == 0 && ((uintptr_t)ea.out & 7) == 0;
+  if (EPI == EPI_RESID_ATTN)
+    return (ea.ldr & 3) == 0 && (((uintptr_t)ea.x | (uintptr_t)ea.x0) & 7) == 0;
+  if (EPI == EPI_RESID_MLP) return (ea.ldr & 3) == 0 && ((uintptr_t)ea.x & 7) == 0;
+  return (ea.ldz & 3) == 0 && ((uintptr_t)ea.z & 7) == 0 && ((uintptr_t)ea.logits & 15) == 0;
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue4(const EpiArgs& ea, bool vec, int m, int n, int N,
+                                          const floatx4_t& y) {
+  if (!vec || n + 3 >= N) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) epilogue<EPI>(ea, m, n + r, y[r]);
+    return;
+  }
+  if (EPI == EPI_STORE) {
+    *(uint2*)(ea.out + (size_t)m * ea.ldo + n) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+  } else if (EPI == EPI_RELU2) {
+    const uint32_t a = relu2_bf(y[0]) | ((uint32_t)relu2_bf(y[1]) << 16);
+    const uint32_t b = relu2_bf(y[2]) | ((uint32_t)relu2_bf(y[3]) << 16);
+    *(uint2*)(ea.out + (size_t)m * ea.ldo + n) = make_uint2(a, b);
+  } else if (EPI == EPI_RESID_ATTN || EPI == EPI_RESID_MLP) {
+    const size_t i = (size_t)m * ea.ldr + n;
+    const uint2 xv = *(const uint2*)(ea.x + i);
+    const float xf[4] = {__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                         __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u)};
+    bf16_t o[4];
+    if (EPI == EPI_RESID_ATTN) {
+      const uint2 zv = *(const uint2*)(ea.x0 + i);
+      const float zf[4] = {__uint_as_float(zv.x << 16), __uint_as_float(zv.x & 0xffff0000u),
+                           __uint_as_float(zv.y << 16), __uint_as_float(zv.y & 0xffff0000u)};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = mix_attn(ea.lam, xf[r], zf[r], y[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = mix_mlp(ea.lam, xf[r], y[r]);
+    }
+    *(uint2*)(ea.x + i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+  } else {  // EPI_LOGITS
+    bf16_t z[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[r] = f2bf(y[r]);
+    const size_t i = (size_t)m * ea.ldz + n;
+    if (ea.z) *(uint2*)(ea.z + i) = make_uint2(z[0] | ((uint32_t)z[1] << 16), z[2] | ((uint32_t)z[3] << 16));
+    if (ea.logits)
+      *(float4*)(ea.logits + i) = make_float4(softcap(bf2f(z[0])), softcap(bf2f(z[1])),
+                                              softcap(bf2f(z[2])), softcap(bf2f(z[3])));
+  }
+}
+
 // ---- GEMV -------------------------------------------------------------------
 
 constexpr int GEMV_THREADS = 256;
@@ -291,6 +348,80 @@ hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int
 
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64, GM_LDS = GM_BK + 8;  // +16 B row pad
 
+// QKV epilogue of one BM x 128 tile whose bf16 values are staged in LDS
+// (row pitch 136): two threads per row take 64 columns each.  A tile lies in
+// one section (q, k or v) and holds one head (Dh 128) or two (Dh 64).  q and
+// k: fp32 sum of squares over the head, x * rsqrt(mean + eps) rounded to
+// bf16, then the dim pairs below Dh/4 rotated by the RoPE table row of the
+// token's position (model.py:244-247); v is copied.  16-byte stores.
+template <int BM>
+__device__ __forceinline__ void qkv_tile_epilogue(const EpiArgs& ea, const bf16_t* tile, int m0,
+                                                  int n0, int M, int tid) {
+  constexpr int CP = GM_BN + 8;
+  const int Dh = ea.Dh, d = ea.H * Dh, D4 = Dh / 4;
+  const int sec = n0 / d;                   // 0 q, 1 k, 2 v
+  const int half = tid & 1;
+  const int head = (n0 - sec * d) / Dh + (Dh == 64 ? half : 0);
+  // this thread's two 32-dim runs inside its head: the rotated pairs (dims
+  // below Dh/2) are the first run, split evenly between the two threads of a
+  // row for Dh 128 (dims 32h.. and 64 + 32h..), the head's halves for Dh 64
+  const int d0 = Dh == 128 ? 32 * half : 0;
+  const int d1 = Dh == 128 ? 64 + 32 * half : 32;
+  const int c0 = Dh == 128 ? 32 * half : 64 * half;   // tile columns of the runs
+  const int c1 = c0 + (Dh == 128 ? 64 : 32);
+  for (int rr = tid >> 1; rr < BM; rr += 128) {
+    const int m = m0 + rr;
+    if (m >= M) continue;                   // both threads of a pair skip together
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[u] = *(const uint4*)(tile + rr * CP + c0 + u * 8);
+      v[4 + u] = *(const uint4*)(tile + rr * CP + c1 + u * 8);
+    }
+    const int b = m / ea.T, t = m - b * ea.T;
+    const int ps = ea.pos[b] + t;
+    if (sec < 2) {
+      float f[64];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) unpack8(v[u], f + 8 * u);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 64; ++e) ss += f[e] * f[e];
+      if (Dh == 128) ss += __shfl_xor(ss, 1, 64);
+      const float r = rsqrtf(ss / (float)Dh + ea.eps);
+#pragma unroll
+      for (int e = 0; e < 64; ++e) f[e] = rbf(f[e] * r);
+      // pairs d0/2 .. d0/2 + 15 are all below Dh/4: rotate them
+      const float4* cp = (const float4*)(ea.cs + (size_t)ps * D4 + d0 / 2);
+      const float4* sp = (const float4*)(ea.sn + (size_t)ps * D4 + d0 / 2);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 c4 = cp[g], s4 = sp[g];
+        const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ssn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int jp = 4 * g + e;
+          const float a0 = f[2 * jp], a1 = f[2 * jp + 1];
+          f[2 * jp] = cc[e] * a0 + ssn[e] * a1;
+          f[2 * jp + 1] = cc[e] * a1 - ssn[e] * a0;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = make_uint4(pack2(f[8 * u], f[8 * u + 1]), pack2(f[8 * u + 2], f[8 * u + 3]),
+                          pack2(f[8 * u + 4], f[8 * u + 5]), pack2(f[8 * u + 6], f[8 * u + 7]));
+    }
+    bf16_t* hb = sec == 0 ? ea.out + (size_t)m * ea.ldo + head * Dh
+                          : (sec == 1 ? ea.kc : ea.vc) +
+                                (((size_t)b * ea.H + head) * ea.max_ctx + ps) * Dh;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      *(uint4*)(hb + d0 + u * 8) = v[u];
+      *(uint4*)(hb + d1 + u * 8) = v[4 + u];
+    }
+  }
+}
+
 // BM = 128 for prefill; BM = 64 when M <= 64 (no padding rows in the MFMAs:
 // the batch-64 lm_head runs 1.4x faster measured).
 template <int EPI, int BM>
@@ -299,8 +430,9 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
                                               EpiArgs ea) {
   constexpr int AC = BM * GM_BK / 8 / 256;   // 16-byte A chunks per thread per K tile
   constexpr int WM = BM / 2, MT = WM / 16;   // rows per wave, 16-row MFMA tiles per wave
-  __shared__ __attribute__((aligned(16))) bf16_t As[BM * GM_LDS];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[GM_BN * GM_LDS];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[(BM + GM_BN) * GM_LDS];
+  bf16_t* As = smem;
+  bf16_t* Bs = smem + BM * GM_LDS;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv >> 1, wn = wv & 1;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * GM_BN;
@@ -334,11 +466,18 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
     for (int i = 0; i < 4; ++i) *(uint4*)(Bs + arow[i] * GM_LDS + acol[i]) = rb[i];
   };
 
-  floatx4_t acc[MT][4];
+  // SWAP: acc[j][i] is block (N block j, M block i) of C^T = W A^T, so that a
+  // lane holds four consecutive columns n of one row m (8-byte epilogue
+  // accesses); otherwise block (M block i, N block j) of C = A W^T, a lane
+  // holding one column of four rows.  Measured: the read-modify-write
+  // epilogues gain from SWAP (prefill o / proj 20 us each), the plain stores
+  // lose (qkv / fc 16 us each).
+  constexpr bool SWAP = EPI != EPI_STORE && EPI != EPI_RELU2;
+  floatx4_t acc[4][MT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MT; ++i) acc[j][i] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
 
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
   load_tile(0);
@@ -356,26 +495,64 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         b[j] = *(const bf16x8_t*)(Bs + (wn * 64 + j * 16 + r16) * GM_LDS + kk + kq);
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
+      if constexpr (SWAP) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-  }
-  // C layout of 16x16 MFMA: lane holds column (lane & 15), rows 4*(lane>>4) + r
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+          for (int i = 0; i < MT; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a[i], acc[j][i], 0, 0, 0);
+      } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 64 + j * 16 + r16;
-      if (n >= N) continue;
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + r;
-        if (m < M) epilogue<EPI>(ea, m, n, acc[i][j][r]);
+          for (int j = 0; j < 4; ++j)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
       }
     }
+  }
+  if constexpr (!SWAP) {
+    // C layout of the 16x16 MFMA: lane holds column (lane & 15), rows 4 (lane >> 4) + r
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + j * 16 + r16;
+        if (n >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + r;
+          if (m < M) epilogue<EPI>(ea, m, n, acc[j][i][r]);
+        }
+      }
+    return;
+  }
+  // C^T layout: lane holds column m = (lane & 15) of its M block and rows
+  // n = 4 (lane >> 4) + r, r = 0..3, of its N block
+  if constexpr (EPI == EPI_QKV) {
+    __syncthreads();   // every wave is done with the last K tile in LDS
+    constexpr int CP = GM_BN + 8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const floatx4_t y = acc[j][i];
+        *(uint2*)(smem + (wm * WM + i * 16 + r16) * CP + wn * 64 + j * 16 + (lane >> 4) * 4) =
+            make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    __syncthreads();
+    qkv_tile_epilogue<BM>(ea, smem, m0, n0, M, tid);
+  } else {
+    const bool vec = epi_vec_ok<EPI>(ea);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 64 + j * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = m0 + wm * WM + i * 16 + r16;
+        if (m < M) epilogue4<EPI>(ea, vec, m, n, N, acc[j][i]);
+      }
+    }
+  }
 }
 
 // ---- skinny MFMA GEMM (decode, M <= 128) ------------------------------------
@@ -563,6 +740,15 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
   return hipGetLastError();
 }
 
+// The fused QKV epilogue needs every 128-column tile inside one section and
+// whole heads per tile: d = H * Dh a multiple of 128, Dh 64 or 128.
+bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea) {
+  const int d = ea.H * ea.Dh;
+  return M > 0 && K % GM_BK == 0 && (ea.Dh == 64 || ea.Dh == 128) && d % GM_BN == 0 &&
+         N == 3 * d && ea.T > 0 && M % ea.T == 0 && ea.ldo % 8 == 0 && ea.out && ea.kc &&
+         ea.vc && ea.pos && ea.cs && ea.sn;
+}
+
 hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                 const EpiArgs& ea, hipStream_t st) {
   if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
@@ -580,6 +766,9 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
     case EPI_RESID_ATTN: ANN_GM(EPI_RESID_ATTN)
     case EPI_RESID_MLP: ANN_GM(EPI_RESID_MLP)
     case EPI_LOGITS: ANN_GM(EPI_LOGITS)
+    case EPI_QKV:
+      if (!gemm_qkv_fits(M, N, K, ea)) return hipErrorInvalidValue;
+      ANN_GM(EPI_QKV)
     default:
       return hipErrorInvalidValue;
   }
