@@ -57,6 +57,7 @@ SIGNATURES = {
     "ann_bind": (ctypes.c_int, [_P, _P, _SZ, _P, _SZ, _P, _SZ]),
     "ann_reset": (ctypes.c_int, [_P]),
     "ann_forward_logits": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
+    "ann_forward_loss": (ctypes.c_int, [_P, _P, _P, _I, _I, _P, _P, _P]),
     "ann_prefill": (ctypes.c_int, [_P, _P, _I, _I, ctypes.POINTER(AnnSampling), _P, _P, _P]),
     "ann_decode_step": (ctypes.c_int, [_P, _P, _I, ctypes.POINTER(AnnSampling), _P, _P, _P]),
     "ann_context_length": (ctypes.c_int, [_P]),

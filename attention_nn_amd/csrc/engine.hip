@@ -74,7 +74,8 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes, total;
+  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes, ce,
+      ce_tz, ce_rows, ce_mean, total;
 };
 
 // Exchange area of the persistent decode step (batch 1): tagged words of
@@ -95,6 +96,9 @@ size_t pd_layout(const ann_config& c, int which) {
   return off;
 }
 
+// 128-column tiles of the lm_head GEMM (its work-group tile width).
+int ce_tiles(const ann_config& c) { return (c.V + 127) / 128; }
+
 SLayout ws_layout(const ann_config& c) {
   const size_t d = c.d, M = c.max_tokens, B = c.max_batch, Dh = d / c.H;
   SLayout s{};
@@ -114,6 +118,12 @@ SLayout ws_layout(const ann_config& c) {
   s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
   s.zb = off; off += up(B * (size_t)c.V * 2);
   s.pd = off; off += (s.pd_bytes = up(pd_layout(c, 0)));
+  // training-forward loss: per-(128-column tile, row) partial sums, target
+  // logits, per-row losses, the mean
+  s.ce = off; off += up((size_t)ce_tiles(c) * M * 4);
+  s.ce_tz = off; off += up(M * 4);
+  s.ce_rows = off; off += up(M * 4);
+  s.ce_mean = off; off += up(4);
   s.total = off;
   return s;
 }
@@ -230,8 +240,10 @@ bool proj_is_gemm(int M, int N, int K, int pre) {
 
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st) {
-  const bool use_gemv = gemv_fits(M, K);
-  const bool use_sk = !use_gemv && !proj_is_gemm(M, N, K, pre);
+  // the QKV and CE epilogues exist on the MFMA GEMM only
+  const bool gemm_only = epi == EPI_CE;
+  const bool use_gemv = !gemm_only && gemv_fits(M, K);
+  const bool use_sk = !gemm_only && !use_gemv && !proj_is_gemm(M, N, K, pre);
   if (epi == EPI_QKV && (use_gemv || use_sk)) return fail(ANN_E_ARG, "fused QKV needs the MFMA GEMM");
   if (pre == PRE_RMS && !use_gemv && !use_sk) {   // large GEMM: A normalised once into h
     if (K > c->c.d) return fail(ANN_E_ARG, "RMS prologue wider than the model dim");
@@ -730,6 +742,34 @@ int ann_forward_logits(ann_ctx* c, const int32_t* tokens, int32_t B, int32_t T, 
   rc = proj(c, ANN_PROF_LM_HEAD, EPI_LOGITS, PRE_RMS, c->wptr(c->wl.head), c->sp<bf16_t>(c->sl.x),
             c->c.d, B * T, c->c.V, c->c.d, ez, st);
   if (rc) return rc;
+  HIPCHK(advance_pos(pos, B, T, st));
+  c->len = T;
+  return ANN_OK;
+}
+
+int ann_forward_loss(ann_ctx* c, const int32_t* tokens, const int32_t* targets, int32_t B,
+                     int32_t T, float* loss, float* row_loss, void* stream) {
+  int rc = check_prefill_shape(c, tokens, B, T);
+  if (rc) return rc;
+  if (!targets || !loss) return fail(ANN_E_ARG, "targets / loss is null");
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* pos = c->sp<int32_t>(c->sl.pos);
+  HIPCHK(set_pos(pos, B, 0, st));
+  c->len = 0;
+  c->B = B;
+  rc = run_body(c, tokens, B, T, st);
+  if (rc) return rc;
+  const int M = B * T;
+  EpiArgs ec{};
+  ec.ce_part = c->sp<float>(c->sl.ce);
+  ec.ce_tz = c->sp<float>(c->sl.ce_tz);
+  ec.tgt = targets;
+  ec.ldz = M;
+  rc = proj(c, ANN_PROF_LM_HEAD, EPI_CE, PRE_RMS, c->wptr(c->wl.head), c->sp<bf16_t>(c->sl.x),
+            c->c.d, M, c->c.V, c->c.d, ec, st);
+  if (rc) return rc;
+  float* rows = row_loss ? row_loss : c->sp<float>(c->sl.ce_rows);
+  HIPCHK(ce_finalize(ec.ce_part, M, ce_tiles(c->c), ec.ce_tz, M, rows, loss, st));
   HIPCHK(advance_pos(pos, B, T, st));
   c->len = T;
   return ANN_OK;

@@ -175,6 +175,40 @@ __global__ void k_qkv_post(const bf16_t* __restrict__ qkv, bf16_t* __restrict__ 
   *(uint32_t*)(vc + cidx) = vw;
 }
 
+// ---- softcapped cross-entropy: per-row loss and the mean --------------------
+//
+// ce_softcap_fwd (metal_kernels.py:153-193) after the lm_head GEMM has left,
+// per 128-column tile t and row m, the partial sum of exp(softcap(z)) in
+// part[t * ld + m] and the target's softcapped logit in tz[m]:
+//   loss[m] = log(sum_t part[t][m]) - tz[m]
+// One thread per row walks the tiles in order (coalesced across rows); the
+// mean (model.py:221) is one work-group summing the rows in a fixed order.
+__global__ void k_ce_rows(const float* __restrict__ part, int ld, int ntiles,
+                          const float* __restrict__ tz, int M, float* __restrict__ rows) {
+  const int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  float sum = 0.f;
+  for (int t = 0; t < ntiles; ++t) sum += part[(size_t)t * ld + m];
+  rows[m] = logf(sum) - tz[m];
+}
+
+constexpr int CE_MEAN_THREADS = 1024;
+
+__global__ __launch_bounds__(CE_MEAN_THREADS) void k_ce_mean(const float* __restrict__ rows, int M,
+                                                            float* __restrict__ mean) {
+  __shared__ float buf[CE_MEAN_THREADS];
+  const int tid = threadIdx.x;
+  float sum = 0.f;
+  for (int m = tid; m < M; m += CE_MEAN_THREADS) sum += rows[m];
+  buf[tid] = sum;
+  __syncthreads();
+  for (int w = CE_MEAN_THREADS / 2; w > 0; w >>= 1) {
+    if (tid < w) buf[tid] += buf[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) *mean = buf[0] / (float)M;
+}
+
 // ---- operators (reference kernel API) ----------------------------------------
 
 template <typename T> __device__ __forceinline__ float ldf(const T* p, size_t i);
@@ -305,6 +339,16 @@ hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const 
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, int M, float* rows,
+                       float* mean, hipStream_t st) {
+  if (M <= 0 || ntiles <= 0 || ld < M || !part || !tz || !rows || !mean)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_ce_rows, dim3(cdiv(M, 256)), dim3(256), 0, st, part, ld, ntiles, tz, M,
+                     rows);
+  hipLaunchKernelGGL(k_ce_mean, dim3(1), dim3(CE_MEAN_THREADS), 0, st, rows, M, mean);
   return hipGetLastError();
 }
 

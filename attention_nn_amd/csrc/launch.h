@@ -17,8 +17,12 @@ namespace ann {
 //                   q = rope(rms(bf16(y_q))) -> out (M, ldo); k = rope(rms(bf16(y_k)))
 //                   and v = bf16(y_v) -> the KV cache at [b][h][pos[b] + t]
 //                   (model.py:244-247, 252)
+//   EPI_CE          (MFMA GEMM only, lm_head of the training forward) per row m and
+//                   128-column tile t: ce_part[t * ldz + m] = sum of exp(softcap(bf16(y)))
+//                   over the tile's columns; ce_tz[m] = softcap(bf16(y[tgt[m]])) from
+//                   the tile holding the target (metal_kernels.py:153-193)
 enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4,
-       EPI_QKV = 5 };
+       EPI_QKV = 5, EPI_CE = 6 };
 
 struct EpiArgs {
   bf16_t* out;       // STORE / RELU2 output (M, ldo)
@@ -43,6 +47,11 @@ struct EpiArgs {
   const float* sn;
   int T, H, Dh, max_ctx;
   float eps;
+  // CE: per-tile partial sums (ldz = row stride of a tile's slice), target
+  // logits, targets
+  float* ce_part;
+  float* ce_tz;
+  const int32_t* tgt;
 };
 
 // Sampling parameters read by the sampler from device memory (so a captured
@@ -80,6 +89,10 @@ hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int
 // rms: A rows RMS-normalised in the kernel (K <= 3072).
 bool gemm_skinny_fits(int M, int N, int K, bool rms);
 bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea);
+// Per-row loss = log(sum over tiles of ce_part) - ce_tz (tiles summed in
+// order), written to rows[M]; mean over the rows (fixed order) to *mean.
+hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, int M, float* rows,
+                       float* mean, hipStream_t st);
 hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
                        int K, float eps, const EpiArgs& ea, hipStream_t st);
 // MFMA GEMM (prefill): y = A @ W^T with A (M, lda) bf16.

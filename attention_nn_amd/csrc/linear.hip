@@ -528,7 +528,46 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
   }
   // C^T layout: lane holds column m = (lane & 15) of its M block and rows
   // n = 4 (lane >> 4) + r, r = 0..3, of its N block
-  if constexpr (EPI == EPI_QKV) {
+  if constexpr (EPI == EPI_CE) {
+    // softcap(bf16(z)) in (0, 23): sum exp(zc) needs no max pass.  Row sums:
+    // in-lane over the wave's 4 N blocks, then over the 4 lane groups, then
+    // the two column halves (wn) through LDS, always in the same order.
+    float rs[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int m = m0 + wm * WM + i * 16 + r16;
+      const int tg = m < M ? ea.tgt[m] : -1;
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = n0 + wn * 64 + j * 16 + (lane >> 4) * 4 + r;
+          if (n < N) {
+            const float zc = softcap(bf2f(f2bf(acc[j][i][r])));
+            sum += __expf(zc);
+            if (n == tg) ea.ce_tz[m] = zc;
+          }
+        }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      rs[i] = sum;
+    }
+    __syncthreads();   // LDS tiles no longer read: reuse for the halves
+    float* red = (float*)smem;
+    if (wn == 1 && lane < 16) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) red[wm * WM + i * 16 + r16] = rs[i];
+    }
+    __syncthreads();
+    if (wn == 0 && lane < 16) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = m0 + wm * WM + i * 16 + r16;
+        if (m < M) ea.ce_part[(size_t)blockIdx.x * ea.ldz + m] = rs[i] + red[wm * WM + i * 16 + r16];
+      }
+    }
+  } else if constexpr (EPI == EPI_QKV) {
     __syncthreads();   // every wave is done with the last K tile in LDS
     constexpr int CP = GM_BN + 8;
 #pragma unroll
@@ -769,6 +808,9 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
     case EPI_QKV:
       if (!gemm_qkv_fits(M, N, K, ea)) return hipErrorInvalidValue;
       ANN_GM(EPI_QKV)
+    case EPI_CE:
+      if (!ea.ce_part || !ea.ce_tz || !ea.tgt || ea.ldz < M) return hipErrorInvalidValue;
+      ANN_GM(EPI_CE)
     default:
       return hipErrorInvalidValue;
   }

@@ -131,6 +131,22 @@ class Engine:
         self.batch = B
         return out
 
+    def forward_loss(self, tokens, targets, rows=False):
+        """GPT.__call__ (model.py:180-221): mean softcapped CE of (B, T) ids
+        against (B, T) targets as a 0-d fp32 device tensor; with ``rows`` also
+        the (B*T,) per-row losses."""
+        t = self._tokens(tokens, 2)
+        g = self._tokens(targets, 2)
+        if tuple(g.shape) != tuple(t.shape):
+            raise ValueError(f"targets {tuple(g.shape)} must match tokens {tuple(t.shape)}")
+        B, T = t.shape
+        mean = torch.empty((), dtype=torch.float32, device=self.device)
+        per = torch.empty((B * T,), dtype=torch.float32, device=self.device) if rows else None
+        _lib.check(_lib.lib().ann_forward_loss(self._ctx, _ptr(t), _ptr(g), B, T, _ptr(mean),
+                                               _ptr(per) if rows else None, _stream()))
+        self.batch = B
+        return (mean, per) if rows else mean
+
     def prefill(self, tokens, temperature=0.0, top_k=0, seed=0, step=0, want_logits=False):
         """Prefill (B, T) prompts; returns (next ids (B,) int32, logits (B,V) or None)."""
         t = self._tokens(tokens, 2)

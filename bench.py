@@ -72,6 +72,12 @@ def prefill_flops(cfg, B, T):
     return f
 
 
+def train_fwd_flops(cfg, B, T):
+    """GPT.__call__: the prefill body plus the lm_head over every row."""
+    d, V = cfg.model_dim, cfg.vocab_size
+    return prefill_flops(cfg, B, T) - 2 * d * V * B + 2 * d * V * B * T
+
+
 def step_traffic():
     """HBM bytes per launch of the persistent decode kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a known-size copy),
@@ -172,6 +178,17 @@ def secondary_b64(cfg, params):
     torch.cuda.synchronize()
     pms = e0.elapsed_time(e1) / reps
     pf = prefill_flops(cfg, B, P)
+    # training forward (GPT.__call__): same tokens, targets = the next ids
+    tg = np.roll(pr, -1, axis=1)
+    loss = eng.forward_loss(pr, tg)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        loss = eng.forward_loss(pr, tg)
+    e1.record()
+    torch.cuda.synchronize()
+    tms = e0.elapsed_time(e1) / reps
+    tfl = train_fwd_flops(cfg, B, P)
     ms64, _, _, toks64 = run_decode(eng, pr, S, 8, 0.8, 50, 7)
     b64_bytes = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
     b64_gbs = b64_bytes / (ms64 / S / 1e3) / 1e9
@@ -185,6 +202,12 @@ def secondary_b64(cfg, params):
         "b64_prefill": {"ms": round(pms, 3), "tok_s": round(B * P / (pms / 1e3), 1),
                         "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_TFLOPS, 4),
                         "flops": pf},
+        "b64_train_fwd": {"ms": round(tms, 3), "tok_s": round(B * P / (tms / 1e3), 1),
+                          "tflops": round(tfl / (tms / 1e3) / 1e12, 2),
+                          "mfma_frac": round(tfl / (tms / 1e3) / 1e12 / MFMA_BF16_TFLOPS, 4),
+                          "flops": tfl, "loss": round(float(loss.item()), 4),
+                          "workload": "GPT.__call__ on the cfg3 prompts (64 x 512), "
+                                      "targets = next ids, loss only"},
     }
 
 

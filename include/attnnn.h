@@ -17,6 +17,10 @@
  *   ann_create / ann_pack_weights / ann_bind  <- GPT(cfg) + params dict
  *                                                (model.py:138-153, sample.py:31-38)
  *   ann_forward_logits                        <- GPT.logits (model.py:223-263)
+ *   ann_forward_loss                          <- GPT.__call__ (model.py:180-221) with the
+ *                                                fused softcap CE (softcap_ce, model.py:
+ *                                                121-132; ce_softcap_fwd, metal_kernels.py:
+ *                                                153-193, 213-221)
  *   ann_prefill / ann_decode_step             <- the per-token loop body
  *                                                (sample.py:42-50: logits of the
  *                                                last row, /temp, top-k, categorical)
@@ -121,6 +125,17 @@ int ann_reset(ann_ctx* ctx);
  * ann_decode_step may follow. */
 int ann_forward_logits(ann_ctx* ctx, const int32_t* tokens, int32_t B, int32_t T,
                        float* logits, void* stream);
+
+/* GPT.__call__ (training forward, loss only): tokens and targets (B, T) int32
+ * on the device, positions 0..T-1.  Writes the mean over the B*T rows of
+ * log(sum_v exp(zc[v])) - zc[target], zc = 23*sigmoid((z + 5)/7.5) and
+ * z = bf16(rms(x) @ lm_head) over all V columns, as one fp32 to *loss, and the
+ * per-row losses (B*T fp32) to row_loss when non-null.  The logits never
+ * reach memory.  Targets must lie in [0, V) (not checked on the device: an
+ * out-of-range target leaves its row's value undefined).  Leaves the KV cache
+ * filled like ann_forward_logits. */
+int ann_forward_loss(ann_ctx* ctx, const int32_t* tokens, const int32_t* targets, int32_t B,
+                     int32_t T, float* loss, float* row_loss, void* stream);
 
 /* Prefill B prompts of T tokens (positions 0..T-1), then sample one token
  * per sequence into out_tok (B).  logits (B, V) of the last rows is written

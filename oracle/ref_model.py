@@ -1,9 +1,11 @@
 """ORACLE -- test infrastructure only.
 
 A CPU (PyTorch fp32) restatement of the reference inference forward
-``GPT.logits`` (``/root/reference/model.py:223-263``) and of the two custom
+``GPT.logits`` (``/root/reference/model.py:223-263``), of the two custom
 Metal kernels it calls (``metal_kernels.py:37-47`` relu2,
-``metal_kernels.py:87-134,144-150`` half-truncated RoPE).  Only ``tests/``,
+``metal_kernels.py:87-134,144-150`` half-truncated RoPE), and of the
+training forward's loss ``GPT.__call__`` (``model.py:180-221``) with its
+fused softcapped cross-entropy (``metal_kernels.py:153-193``).  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may import
 this module, and only as the checker or the timed CPU baseline; the product
 path (``attention_nn_amd``) never calls it.
@@ -34,6 +36,11 @@ Parity status per function (what pins each one; checked in tests/):
   logits (whole)        : closed-form known answer of the degenerate init
                           (Wo = proj = x0 = 0 => x_L is a scaled x0),
                           KV-cache decode == full recompute, fp64 forward
+  softcap_ce            : torch.nn.functional.cross_entropy on the softcapped
+                          logits; uniform z => loss = log V exactly
+  attention(banded_bf16): within bf16 rounding of the fp64 brute force
+  loss (whole)          : composition of the pinned parts; equals the mean
+                          of softcap_ce over the rows of the pinned logits
 """
 
 import math
@@ -118,8 +125,21 @@ def keep_mask(q_pos, k_pos, long_layer, window):
     return keep
 
 
-def attention(q, k, v, keep, scale, mlx_fallback_attn=False):
-    """q (B,H,Tq,Dh), k/v (B,H,Tk,Dh) bf16-valued fp32; keep (Tq,Tk) bool."""
+def attention(q, k, v, keep, scale, mlx_fallback_attn=False, banded_bf16=False):
+    """q (B,H,Tq,Dh), k/v (B,H,Tk,Dh) bf16-valued fp32; keep (Tq,Tk) bool.
+
+    ``banded_bf16`` restates the training forward's block-banded attention
+    (model.py:171-178): the scores come out of a bf16 matmul and are scaled in
+    bf16, the -30000 additive mask zeroes the dropped keys exactly (exp
+    underflows in fp32), softmax(precise=True) runs in fp32 and returns bf16,
+    and P.V is a bf16 matmul.  The 512-query bands (model.py:155-169) never
+    drop an allowed key (ks = max(0, qs - W) <= i - W + 1), so the band
+    structure itself changes nothing and is not restated."""
+    if banded_bf16:
+        s = bf(bf(q @ k.transpose(-1, -2)) * scale)
+        s = s.masked_fill(~keep, float("-inf"))
+        p = bf(torch.softmax(s, dim=-1))
+        return bf(p @ v)
     if mlx_fallback_attn:
         s = bf(bf(q * scale) @ k.transpose(-1, -2))
         s = s.masked_fill(~keep, float("-inf"))
@@ -166,7 +186,8 @@ class KVCache:
         return 0 if self.k[0] is None else self.k[0].shape[2]
 
 
-def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=False):
+def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=False,
+            banded_bf16=False):
     """Forward of ``tokens`` (B,T) placed at positions [start, start+T) where
     start = cache.length (0 without a cache).  Returns softcapped fp32 logits
     (B,T,V).  With ``cache`` the new K/V are appended (KV-cache decode);
@@ -197,7 +218,8 @@ def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=Fal
                 v = torch.cat([cache.v[l], v], dim=2)
             cache.k[l], cache.v[l] = k, v
         keep = keep_mask(pos, kpos, l in cfg.long_layers, cfg.window)   # :248-250
-        y = attention(q, k, v, keep, cfg.attn_scale, mlx_fallback_attn)  # :251-254
+        y = attention(q, k, v, keep, cfg.attn_scale, mlx_fallback_attn,  # :251-254
+                      banded_bf16)
         y = bf(y.transpose(1, 2).reshape(B, T, d) @ prep.wo[l])        # :255
         r0, p0, xl = prep.resid[l, 0], prep.post[l, 0], prep.x0l[l]
         x = bf(bf(bf(r0 * x) + bf(p0 * y)) + bf(xl * x0))            # :256
@@ -211,6 +233,28 @@ def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=Fal
     if return_hidden:
         return out, z, hfin
     return out
+
+
+def softcap_ce(z, targets):
+    """Fused softcapped cross-entropy of ``ce_softcap_fwd`` (metal_kernels.py:
+    153-193; pure-MLX form model.py:104-110): per row of z (N, V), in fp32,
+    zc = 23 sigmoid((z + 5) / 7.5), lse = log sum exp(zc) over all V columns,
+    loss = lse - zc[target].  Returns (loss (N,), lse (N,))."""
+    zc = softcap(z)
+    lse = torch.logsumexp(zc, dim=-1)
+    tl = zc.gather(-1, torch.as_tensor(targets, dtype=torch.long)[:, None]).squeeze(-1)
+    return lse - tl, lse
+
+
+def loss(cfg, params, tokens, targets, banded_bf16=True):
+    """``GPT.__call__`` (model.py:180-221): the forward with the training
+    attention, z = bf16(rms(x) @ lm_head) for every row (B*T, V) and the mean
+    softcapped CE.  Returns (mean fp32 scalar, per-row losses (B*T,))."""
+    prep = Prepared(cfg, params)
+    _, z, _ = forward(prep, tokens, None, return_hidden=True, banded_bf16=banded_bf16)
+    rows, _ = softcap_ce(z.reshape(-1, cfg.vocab_size),
+                         torch.as_tensor(targets, dtype=torch.long).reshape(-1))
+    return rows.mean(), rows
 
 
 def logits(cfg, params, tokens, mlx_fallback_attn=False):

@@ -134,6 +134,52 @@ def test_prefill_logits_every_position_long_prompt(dh, window):
     assert err < LOGIT_TOL, err
 
 
+# ---- training forward: GPT.__call__ with the fused softcap CE ---------------
+
+@pytest.mark.parametrize("dh,V,B,T", [(64, 512, 1, 40), (128, 1000, 2, 40), (128, 700, 2, 300)])
+def test_forward_loss_matches_oracle(dh, V, B, T):
+    """GPT.__call__ (model.py:180-221): per-row softcapped CE and the mean
+    against the oracle's training forward (bf16 attention reading) and its
+    fp32 reading.  V = 1000 and 700 leave a partial last 128-column tile;
+    targets include 0 and V - 1."""
+    cfg = GPTConfig(vocab_size=V, num_layers=2, num_heads=2, model_dim=2 * dh, seq_len=320,
+                    window=70, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 29, dense=True))
+    rng = np.random.default_rng(dh + V + T)
+    tok = rng.integers(0, V, (B, T))
+    tgt = rng.integers(0, V, (B, T))
+    tgt[0, 0], tgt[-1, -1] = 0, V - 1
+    print(f"case dh={dh} V={V} B={B} T={T}", flush=True)
+    eng = _engine(cfg, p, B)
+    mean, rows = eng.forward_loss(tok, tgt, rows=True)
+    rows = rows.cpu().double()
+    # measured: rows within 1.4e-3, means within 6e-5 (both readings)
+    for banded in (True, False):
+        rm, rr = R.loss(cfg, p, tok, tgt, banded_bf16=banded)
+        assert (rows - rr.double()).abs().max().item() < 1e-2, banded
+        assert abs(mean.item() - rm.item()) < 5e-4, banded
+    assert abs(mean.item() - rows.mean().item()) < 1e-5
+
+
+def test_forward_loss_equals_cross_entropy_of_own_logits():
+    """Without the oracle: the fused CE epilogue equals torch cross_entropy
+    over the same engine's (B, T, V) softcapped logits (same z, only the
+    summation order of the log-sum-exp differs)."""
+    cfg = small_cfgs()["dh128"]
+    p = perturb_lambdas(init_params(cfg, 37, dense=True))
+    rng = np.random.default_rng(38)
+    tok = rng.integers(0, cfg.vocab_size, (3, 50))
+    tgt = rng.integers(0, cfg.vocab_size, (3, 50))
+    eng = _engine(cfg, p, 3)
+    lg = eng.forward_logits(tok).double()
+    ref = torch.nn.functional.cross_entropy(lg.reshape(-1, cfg.vocab_size),
+                                            torch.from_numpy(tgt).reshape(-1).cuda(),
+                                            reduction="none")
+    mean, rows = eng.forward_loss(tok, tgt, rows=True)
+    assert (rows.double() - ref).abs().max().item() < 1e-4
+    assert abs(mean.item() - ref.mean().item()) < 1e-5
+
+
 @pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 12)])
 def test_decode_teacher_forced_past_window(name, B):
     """Decode logits at every position (well past the window) match the

@@ -221,6 +221,65 @@ def test_kv_cache_decode_equals_full_recompute(tiny_cfg):
     assert (torch.cat(outs, 1) - full).abs().max().item() < 1e-3
 
 
+# ---- training forward: softcapped CE (metal_kernels.py:153-193) -------------
+
+def test_softcap_ce_matches_torch_cross_entropy():
+    """The fused CE restatement against torch's own cross_entropy applied to
+    the softcapped logits (an independent library routine)."""
+    g = torch.Generator().manual_seed(3)
+    z = R.bf(torch.randn(37, 1000, generator=g) * 6)
+    tg = torch.randint(0, 1000, (37,), generator=g)
+    rows, lse = R.softcap_ce(z, tg)
+    ref = torch.nn.functional.cross_entropy(R.softcap(z).double(), tg, reduction="none")
+    assert (rows.double() - ref).abs().max().item() < 1e-5
+    assert (lse.double() - torch.logsumexp(R.softcap(z).double(), -1)).abs().max().item() < 1e-5
+    # a target off by one lands far away
+    bad, _ = R.softcap_ce(z, (tg + 1) % 1000)
+    assert (bad.double() - ref).abs().max().item() > 0.1
+
+
+def test_softcap_ce_uniform_is_log_v():
+    """Equal logits give every class the same softcapped value: loss = log V."""
+    for c in (-30.0, 0.0, 7.5):
+        z = torch.full((3, 50304), c)
+        rows, _ = R.softcap_ce(z, torch.tensor([0, 17, 50303]))
+        assert torch.allclose(rows.double(), torch.full((3,), math.log(50304), dtype=torch.float64),
+                              atol=2e-5)
+
+
+@pytest.mark.parametrize("long_layer", [False, True])
+def test_banded_bf16_attention_brute_force(long_layer):
+    """The training attention reading (bf16 scores and probabilities) stays
+    within bf16 rounding of the fp64 brute force; dropping the scale does not."""
+    rng = np.random.default_rng(321)
+    B, H, T, D, W = 2, 2, 9, 16, 4
+    q, k, v = (rng.normal(0, 0.5, (B, H, T, D)).astype(np.float32) for _ in range(3))
+    q, k, v = (R.bf(torch.from_numpy(a)) for a in (q, k, v))
+    keep = R.keep_mask(torch.arange(T), torch.arange(T), long_layer, W)
+    ref = _attn_brute(q.numpy(), k.numpy(), v.numpy(), 0.1, W, long_layer)
+    got = R.attention(q, k, v, keep, 0.1, banded_bf16=True)
+    assert np.abs(got.numpy() - ref).max() < 1.5e-2
+    unscaled = R.attention(q, k, v, keep, 1.0, banded_bf16=True)
+    assert np.abs(unscaled.numpy() - ref).max() > 5e-2
+
+
+def test_loss_is_torch_cross_entropy_of_the_logits(tiny_cfg):
+    """GPT.__call__'s loss = mean CE of the softcapped logits over every row
+    and all V columns (torch cross_entropy over the pinned logits), and the
+    training attention reading moves it by far less than the tolerance."""
+    p = perturb_lambdas(init_params(tiny_cfg, 13, dense=True))
+    rng = np.random.default_rng(14)
+    tok = rng.integers(0, 512, (2, 24))
+    tgt = rng.integers(0, 512, (2, 24))
+    mean, rows = R.loss(tiny_cfg, p, tok, tgt, banded_bf16=False)
+    lg = R.logits(tiny_cfg, p, tok).reshape(-1, 512).double()
+    ref = torch.nn.functional.cross_entropy(lg, torch.from_numpy(tgt).reshape(-1), reduction="none")
+    assert (rows.double() - ref).abs().max().item() < 1e-5
+    assert abs(mean.item() - ref.mean().item()) < 1e-5
+    mb, _ = R.loss(tiny_cfg, p, tok, tgt, banded_bf16=True)
+    assert abs(mb.item() - mean.item()) < 1e-2
+
+
 # ---- sampler ----------------------------------------------------------------
 
 def test_philox_random123_kat():
