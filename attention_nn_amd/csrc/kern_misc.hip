@@ -181,15 +181,36 @@ __global__ void k_qkv_post(const bf16_t* __restrict__ qkv, bf16_t* __restrict__ 
 // per 128-column tile t and row m, the partial sum of exp(softcap(z)) in
 // part[t * ld + m] and the target's softcapped logit in tz[m]:
 //   loss[m] = log(sum_t part[t][m]) - tz[m]
-// One thread per row walks the tiles in order (coalesced across rows); the
-// mean (model.py:221) is one work-group summing the rows in a fixed order.
-__global__ void k_ce_rows(const float* __restrict__ part, int ld, int ntiles,
-                          const float* __restrict__ tz, int M, float* __restrict__ rows) {
-  const int m = blockIdx.x * blockDim.x + threadIdx.x;
-  if (m >= M) return;
+// A work-group takes 64 rows (one per lane, coalesced across the wave); its
+// four waves each sum a contiguous quarter of the tiles, and the quarters are
+// added in wave order.  The mean (model.py:221) is one work-group summing the
+// rows in a fixed order.
+constexpr int CE_ROWS = 64;
+
+__global__ __launch_bounds__(256) void k_ce_rows(const float* __restrict__ part, int ld,
+                                                 int ntiles, const float* __restrict__ tz, int M,
+                                                 float* __restrict__ rows) {
+  __shared__ float q[4][CE_ROWS];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m = blockIdx.x * CE_ROWS + lane;
+  const int per = (ntiles + 3) / 4;
+  const int t0 = wv * per, t1 = min(ntiles, t0 + per);
   float sum = 0.f;
-  for (int t = 0; t < ntiles; ++t) sum += part[(size_t)t * ld + m];
-  rows[m] = logf(sum) - tz[m];
+  if (m < M) {
+    const float* p = part + m;
+    int t = t0;
+    for (; t + 8 <= t1; t += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(t + u) * ld];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    for (; t < t1; ++t) sum += p[(size_t)t * ld];
+  }
+  q[wv][lane] = sum;
+  __syncthreads();
+  if (wv == 0 && m < M) rows[m] = logf(((q[0][lane] + q[1][lane]) + q[2][lane]) + q[3][lane]) - tz[m];
 }
 
 constexpr int CE_MEAN_THREADS = 1024;
@@ -346,8 +367,8 @@ hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, i
                        float* mean, hipStream_t st) {
   if (M <= 0 || ntiles <= 0 || ld < M || !part || !tz || !rows || !mean)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_ce_rows, dim3(cdiv(M, 256)), dim3(256), 0, st, part, ld, ntiles, tz, M,
-                     rows);
+  hipLaunchKernelGGL(k_ce_rows, dim3(cdiv(M, CE_ROWS)), dim3(256), 0, st, part, ld, ntiles, tz,
+                     M, rows);
   hipLaunchKernelGGL(k_ce_mean, dim3(1), dim3(CE_MEAN_THREADS), 0, st, rows, M, mean);
   return hipGetLastError();
 }
