@@ -42,6 +42,7 @@ class AnnSampling(ctypes.Structure):
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
+_F = ctypes.c_float
 _SZ = ctypes.c_size_t
 
 # name -> (restype, argtypes); every symbol include/attnnn.h declares.
@@ -65,6 +66,13 @@ SIGNATURES = {
     "ann_op_rope_ht": (ctypes.c_int, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "ann_op_rope_tables": (ctypes.c_int, [_P, _P, _I, _I, ctypes.c_float, _P]),
     "ann_op_rms_norm": (ctypes.c_int, [_P, _P, _I, _I, ctypes.c_float, _I, _P]),
+    "ann_op_adam_step": (ctypes.c_int, [_P, _P, _P, _P, _SZ, _F, _F, _F, _F, _F, _P, _P, _P, _P]),
+    "ann_op_muon_momentum": (ctypes.c_int, [_P, _P, _SZ, _F, _P, _P, _P]),
+    "ann_op_muon_apply": (ctypes.c_int, [_P, _P, _SZ, _F, _F, _P, _P]),
+    "ann_op_polar_express_ws_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+    "ann_op_polar_express": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _SZ, _P]),
+    "ann_op_normuon_ws_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+    "ann_op_normuon": (ctypes.c_int, [_P, _P, _I, _I, _I, _F, _P, _P, _SZ, _P]),
     "ann_profile_enable": (ctypes.c_int, [_P, _I, _I]),
     "ann_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(_I)]),
     "ann_check_device": (ctypes.c_int, [_P, _P]),

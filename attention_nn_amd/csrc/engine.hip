@@ -863,4 +863,62 @@ int ann_op_rms_norm(const void* x, void* y, int32_t rows, int32_t dim, float eps
   return ANN_OK;
 }
 
+// ---- optimizer step (muon.py, metal_kernels.py:236-328) -------------------------
+
+int ann_op_adam_step(const float* p, const float* g, const float* m, const float* v, size_t n,
+                     float beta1, float beta2, float eps, float step_size, float eff_wd,
+                     float* p_out, float* m_out, float* v_out, void* stream) {
+  if (n && (!p || !g || !m || !v || !p_out || !m_out || !v_out))
+    return fail(ANN_E_ARG, "null argument");
+  HIPCHK(adam_step(p, g, m, v, n, beta1, beta2, eps, step_size, eff_wd, p_out, m_out, v_out,
+                   (hipStream_t)stream));
+  return ANN_OK;
+}
+
+int ann_op_muon_momentum(const float* g, const float* buf, size_t n, float mu, float* geff,
+                         float* buf_out, void* stream) {
+  if (n && (!g || !buf || !geff || !buf_out)) return fail(ANN_E_ARG, "null argument");
+  HIPCHK(muon_momentum(g, buf, n, mu, geff, buf_out, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+int ann_op_muon_apply(const float* p, const float* u, size_t n, float lr, float wd, float* p_out,
+                      void* stream) {
+  if (n && (!p || !u || !p_out)) return fail(ANN_E_ARG, "null argument");
+  HIPCHK(muon_apply(p, u, n, lr, wd, p_out, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+size_t ann_op_polar_express_ws_bytes(int32_t batch, int32_t M, int32_t N) {
+  return polar_express_ws_bytes(batch, M, N);
+}
+
+int ann_op_polar_express(const float* g, int32_t batch, int32_t M, int32_t N, void* out,
+                         void* ws, size_t ws_bytes, void* stream) {
+  if (!g || !out || !ws) return fail(ANN_E_ARG, "null argument");
+  if (batch <= 0 || batch > 65535 || M <= 0 || N <= 0 || M % 64 || N % 64)
+    return fail(ANN_E_ARG, "bad shape batch=%d M=%d N=%d (M, N multiples of 64)", batch, M, N);
+  if (ws_bytes < polar_express_ws_bytes(batch, M, N))
+    return fail(ANN_E_ARG, "workspace %zu < %zu bytes", ws_bytes,
+                polar_express_ws_bytes(batch, M, N));
+  HIPCHK(polar_express(g, batch, M, N, (bf16_t*)out, ws, ws_bytes, (hipStream_t)stream));
+  return ANN_OK;
+}
+
+size_t ann_op_normuon_ws_bytes(int32_t batch, int32_t M, int32_t N) {
+  return normuon_ws_bytes(batch, M, N);
+}
+
+int ann_op_normuon(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
+                   float beta2, float* out, void* ws, size_t ws_bytes, void* stream) {
+  if (!v || !second_mom || !out || !ws) return fail(ANN_E_ARG, "null argument");
+  if (batch <= 0 || M <= 0 || N <= 0)
+    return fail(ANN_E_ARG, "bad shape batch=%d M=%d N=%d", batch, M, N);
+  if (ws_bytes < normuon_ws_bytes(batch, M, N))
+    return fail(ANN_E_ARG, "workspace %zu < %zu bytes", ws_bytes, normuon_ws_bytes(batch, M, N));
+  HIPCHK(normuon((const bf16_t*)v, second_mom, batch, M, N, beta2, out, ws, ws_bytes,
+                 (hipStream_t)stream));
+  return ANN_OK;
+}
+
 }  // extern "C"

@@ -21,8 +21,11 @@ namespace ann {
 //                   128-column tile t: ce_part[t * ldz + m] = sum of exp(softcap(bf16(y)))
 //                   over the tile's columns; ce_tz[m] = softcap(bf16(y[tgt[m]])) from
 //                   the tile holding the target (metal_kernels.py:153-193)
+//   EPI_PE_B        (Polar Express) out = bf16(bf16(s0*x) + bf16(s1*bf16(y)))  (muon.py:37)
+//   EPI_PE_X        (Polar Express) out = bf16(bf16(s0*x) + bf16(y))           (muon.py:38,42)
+//                   x is the epilogue's second operand (M, ldr)
 enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4,
-       EPI_QKV = 5, EPI_CE = 6 };
+       EPI_QKV = 5, EPI_CE = 6, EPI_PE_B = 7, EPI_PE_X = 8 };
 
 struct EpiArgs {
   bf16_t* out;       // STORE / RELU2 output (M, ldo)
@@ -52,6 +55,8 @@ struct EpiArgs {
   float* ce_part;
   float* ce_tz;
   const int32_t* tgt;
+  // PE_B / PE_X scalars
+  float s0, s1;
 };
 
 // Sampling parameters read by the sampler from device memory (so a captured
@@ -89,6 +94,25 @@ hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int
 // rms: A rows RMS-normalised in the kernel (K <= 3072).
 bool gemm_skinny_fits(int M, int N, int K, bool rms);
 bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea);
+// k_gemm over `batch` independent problems (blockIdx.z); epilogues STORE,
+// PE_B, PE_X; sOut / sX are the batch strides of ea.out / ea.x.
+hipError_t gemm_batched(int epi, const bf16_t* A, int lda, long long sA, const bf16_t* W,
+                        long long sW, int M, int N, int K, const EpiArgs& ea, long long sOut,
+                        long long sX, int batch, hipStream_t st);
+// Optimizer step (optim.hip).
+hipError_t adam_step(const float* p, const float* g, const float* m, const float* v, size_t n,
+                     float b1, float b2, float eps, float step, float wd, float* po, float* mo,
+                     float* vo, hipStream_t st);
+hipError_t muon_momentum(const float* g, const float* buf, size_t n, float mu, float* geff,
+                         float* bo, hipStream_t st);
+hipError_t muon_apply(const float* p, const float* u, size_t n, float lr, float wd, float* po,
+                      hipStream_t st);
+size_t polar_express_ws_bytes(int batch, int M, int N);
+hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, void* ws,
+                         size_t ws_bytes, hipStream_t st);
+size_t normuon_ws_bytes(int batch, int M, int N);
+hipError_t normuon(const bf16_t* v, float* second_mom, int batch, int M, int N, float beta2,
+                   float* out, void* ws, size_t ws_bytes, hipStream_t st);
 // Per-row loss = log(sum over tiles of ce_part) - ce_tz (tiles summed in
 // order), written to rows[M]; mean over the rows (fixed order) to *mean.
 hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, int M, float* rows,

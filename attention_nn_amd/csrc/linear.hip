@@ -28,6 +28,12 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
   } else if (EPI == EPI_RESID_MLP) {
     const size_t i = (size_t)m * ea.ldr + n;
     ea.x[i] = mix_mlp(ea.lam, bf2f(ea.x[i]), y);
+  } else if (EPI == EPI_PE_B) {
+    const size_t i = (size_t)m * ea.ldr + n;
+    ea.out[(size_t)m * ea.ldo + n] = f2bf(rbf(ea.s0 * bf2f(ea.x[i])) + rbf(ea.s1 * rbf(y)));
+  } else if (EPI == EPI_PE_X) {
+    const size_t i = (size_t)m * ea.ldr + n;
+    ea.out[(size_t)m * ea.ldo + n] = f2bf(rbf(ea.s0 * bf2f(ea.x[i])) + rbf(y));
   } else {  // EPI_LOGITS
     const bf16_t z = f2bf(y);
     const size_t i = (size_t)m * ea.ldz + n;
@@ -46,6 +52,8 @@ __device__ __forceinline__ bool epi_vec_ok(const EpiArgs& ea) {
   if (EPI == EPI_RESID_ATTN)
     return (ea.ldr & 3) == 0 && (((uintptr_t)ea.x | (uintptr_t)ea.x0) & 7) == 0;
   if (EPI == EPI_RESID_MLP) return (ea.ldr & 3) == 0 && ((uintptr_t)ea.x & 7) == 0;
+  if (EPI == EPI_PE_B || EPI == EPI_PE_X)
+    return ((ea.ldr | ea.ldo) & 3) == 0 && (((uintptr_t)ea.x | (uintptr_t)ea.out) & 7) == 0;
   return (ea.ldz & 3) == 0 && ((uintptr_t)ea.z & 7) == 0 && ((uintptr_t)ea.logits & 15) == 0;
 }
 
@@ -81,6 +89,16 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, bool vec, int m, in
       for (int r = 0; r < 4; ++r) o[r] = mix_mlp(ea.lam, xf[r], y[r]);
     }
     *(uint2*)(ea.x + i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+  } else if (EPI == EPI_PE_B || EPI == EPI_PE_X) {
+    const uint2 xv = *(const uint2*)(ea.x + (size_t)m * ea.ldr + n);
+    const float xf[4] = {__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                         __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u)};
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      o[r] = EPI == EPI_PE_B ? rbf(ea.s0 * xf[r]) + rbf(ea.s1 * rbf(y[r]))
+                             : rbf(ea.s0 * xf[r]) + rbf(y[r]);
+    *(uint2*)(ea.out + (size_t)m * ea.ldo + n) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
   } else {  // EPI_LOGITS
     bf16_t z[4];
 #pragma unroll
@@ -425,9 +443,9 @@ __device__ __forceinline__ void qkv_tile_epilogue(const EpiArgs& ea, const bf16_
 // BM = 128 for prefill; BM = 64 when M <= 64 (no padding rows in the MFMAs:
 // the batch-64 lm_head runs 1.4x faster measured).
 template <int EPI, int BM>
-__global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int lda,
-                                              const bf16_t* __restrict__ W, int M, int N, int K,
-                                              EpiArgs ea) {
+__device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
+                                          const bf16_t* __restrict__ W, int M, int N, int K,
+                                          const EpiArgs& ea) {
   constexpr int AC = BM * GM_BK / 8 / 256;   // 16-byte A chunks per thread per K tile
   constexpr int WM = BM / 2, MT = WM / 16;   // rows per wave, 16-row MFMA tiles per wave
   __shared__ __attribute__((aligned(16))) bf16_t smem[(BM + GM_BN) * GM_LDS];
@@ -592,6 +610,26 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
       }
     }
   }
+}
+
+template <int EPI, int BM>
+__global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int lda,
+                                              const bf16_t* __restrict__ W, int M, int N, int K,
+                                              EpiArgs ea) {
+  gemm_body<EPI, BM>(A, lda, W, M, N, K, ea);
+}
+
+// Batched: blockIdx.z selects matrix z; A, W, the output and the epilogue's
+// second operand (x) advance by their batch strides.
+template <int EPI, int BM>
+__global__ __launch_bounds__(256) void k_gemm_bat(const bf16_t* __restrict__ A, int lda,
+                                                  long long sA, const bf16_t* __restrict__ W,
+                                                  long long sW, int M, int N, int K, EpiArgs ea,
+                                                  long long sOut, long long sX) {
+  const long long z = blockIdx.z;
+  ea.out += z * sOut;
+  ea.x += z * sX;
+  gemm_body<EPI, BM>(A + z * sA, lda, W + z * sW, M, N, K, ea);
 }
 
 // ---- skinny MFMA GEMM (decode, M <= 128) ------------------------------------
@@ -776,6 +814,31 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
 #undef ANN_SK_KB
 #undef ANN_SK_T
 #undef ANN_SK
+  return hipGetLastError();
+}
+
+hipError_t gemm_batched(int epi, const bf16_t* A, int lda, long long sA, const bf16_t* W,
+                        long long sW, int M, int N, int K, const EpiArgs& ea, long long sOut,
+                        long long sX, int batch, hipStream_t st) {
+  if (K % GM_BK != 0 || M <= 0 || N <= 0 || batch <= 0 || batch > 65535)
+    return hipErrorInvalidValue;
+  const int bm = M <= 64 ? 64 : GM_BM;
+  dim3 grid((N + GM_BN - 1) / GM_BN, (M + bm - 1) / bm, batch);
+#define ANN_GB(E)                                                                              \
+  if (bm == 64)                                                                                \
+    hipLaunchKernelGGL((k_gemm_bat<E, 64>), grid, dim3(256), 0, st, A, lda, sA, W, sW, M, N,   \
+                       K, ea, sOut, sX);                                                       \
+  else                                                                                         \
+    hipLaunchKernelGGL((k_gemm_bat<E, GM_BM>), grid, dim3(256), 0, st, A, lda, sA, W, sW, M,   \
+                       N, K, ea, sOut, sX);                                                    \
+  break;
+  switch (epi) {
+    case EPI_STORE: ANN_GB(EPI_STORE)
+    case EPI_PE_B: ANN_GB(EPI_PE_B)
+    case EPI_PE_X: ANN_GB(EPI_PE_X)
+    default: return hipErrorInvalidValue;
+  }
+#undef ANN_GB
   return hipGetLastError();
 }
 

@@ -1,0 +1,390 @@
+// Optimizer step of the training loop: MuonAdam (muon.py:66-137) and its
+// fused kernels (metal_kernels.py:236-328).
+//
+//  * k_adam, k_muon_momentum, k_muon_apply: fp32 elementwise, 16-byte
+//    accesses, HBM-bound.  Same arithmetic and the same comparisons (cautious
+//    weight decay) as the reference kernels.
+//  * Polar Express (muon.py:28-44) on a batch of (M, N) matrices: x = bf16(g /
+//    (||g||_F * 1.02 + 1e-6)), then five iterations of bf16 products on the
+//    MFMA GEMM (batched over blockIdx.z).  Every product is an "NT" GEMM of
+//    k_gemm: x x^T directly; A A because A is symmetric; B x through one
+//    transpose of x per iteration (x B for tall matrices, B symmetric).  The
+//    combinations b A + c A^2 and a x + B x run in the GEMM epilogues with the
+//    eager rounding of each op.
+//  * NorMuon (muon.py:47-63): mean of squares along the reduced axis, one
+//    work-group per matrix for the norms and the second-moment update, then
+//    the broadcast scale.
+// All reductions run in a fixed order: results are bit-reproducible.
+#include <math.h>
+#include <string.h>
+#include "common.h"
+#include "launch.h"
+
+namespace ann {
+
+namespace {
+unsigned grid_for(size_t n, unsigned threads) {
+  size_t g = (n + threads - 1) / threads;
+  if (g > 65536) g = 65536;
+  return g ? (unsigned)g : 1u;
+}
+}  // namespace
+
+// ---- elementwise --------------------------------------------------------------
+
+// adam_step (metal_kernels.py:241-259): fp32 moments, cautious weight decay.
+__device__ __forceinline__ void adam1(float pv, float gv, float m, float v, float b1, float b2,
+                                      float eps, float step, float wd, float& po, float& mo,
+                                      float& vo) {
+  const float mv = b1 * m + (1.0f - b1) * gv;
+  const float vv = b2 * v + (1.0f - b2) * gv * gv;
+  float u = mv / (sqrtf(vv) + eps) * step;
+  if (u * pv > 0.0f) u += pv * wd;
+  po = pv - u;
+  mo = mv;
+  vo = vv;
+}
+
+__global__ void k_adam(const float* __restrict__ p, const float* __restrict__ g,
+                       const float* __restrict__ m, const float* __restrict__ v, size_t n,
+                       float b1, float b2, float eps, float step, float wd, float* __restrict__ po,
+                       float* __restrict__ mo, float* __restrict__ vo) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    adam1(p[i], g[i], m[i], v[i], b1, b2, eps, step, wd, po[i], mo[i], vo[i]);
+}
+
+// muon_momentum (metal_kernels.py:277-290): buf <- lerp(buf, g, 1 - mu),
+// geff <- lerp(g, buf, mu).
+__global__ void k_muon_momentum(const float* __restrict__ g, const float* __restrict__ buf,
+                                size_t n, float mu, float* __restrict__ geff,
+                                float* __restrict__ bo) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gv = g[i], b = buf[i];
+    const float bv = b + (1.0f - mu) * (gv - b);
+    bo[i] = bv;
+    geff[i] = gv + mu * (bv - gv);
+  }
+}
+
+// muon_apply (metal_kernels.py:306-319): decay where u and p agree in sign.
+__global__ void k_muon_apply(const float* __restrict__ p, const float* __restrict__ u, size_t n,
+                             float lr, float wd, float* __restrict__ po) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float uv = u[i];
+    float pv = p[i];
+    if (uv * pv >= 0.0f) pv -= pv * wd * lr;
+    po[i] = pv - uv * lr;
+  }
+}
+
+// ---- Polar Express ------------------------------------------------------------
+
+constexpr int PE_CHUNK = 65536;   // elements per partial sum of squares
+constexpr int PE_THREADS = 256;
+
+// Partial sums of squares: block (chunk c, matrix z) over its PE_CHUNK elements.
+__global__ __launch_bounds__(PE_THREADS) void k_pe_sumsq(const float* __restrict__ g, size_t mn,
+                                                         int nch, float* __restrict__ part) {
+  __shared__ float red[PE_THREADS];
+  const int c = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
+  const float* gz = g + (size_t)z * mn;
+  const size_t e0 = (size_t)c * PE_CHUNK, e1 = min(mn, e0 + PE_CHUNK);
+  float s = 0.f;
+  for (size_t i = e0 + tid; i < e1; i += PE_THREADS) s += gz[i] * gz[i];
+  red[tid] = s;
+  __syncthreads();
+  for (int w = PE_THREADS / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) part[(size_t)z * nch + c] = red[0];
+}
+
+// x = bf16(g / (sqrt(sum) * 1.02 + 1e-6)), the partials summed in order.
+__global__ void k_pe_scale(const float* __restrict__ g, size_t mn, int nch,
+                           const float* __restrict__ part, bf16_t* __restrict__ x) {
+  const int z = blockIdx.y;
+  float s = 0.f;
+  for (int c = 0; c < nch; ++c) s += part[(size_t)z * nch + c];
+  const float den = sqrtf(s) * 1.02f + 1e-6f;
+  const float* gz = g + (size_t)z * mn;
+  bf16_t* xz = x + (size_t)z * mn;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride)
+    xz[i] = f2bf(gz[i] / den);
+}
+
+// dst (C, R) = src (R, C)^T per matrix, 64 x 64 tiles through LDS.
+constexpr int TR_T = 64;
+__global__ __launch_bounds__(256) void k_transpose_bf16(const bf16_t* __restrict__ src,
+                                                        bf16_t* __restrict__ dst, int R, int C) {
+  __shared__ bf16_t t[TR_T][TR_T + 2];
+  const int z = blockIdx.z;
+  const int r0 = blockIdx.y * TR_T, c0 = blockIdx.x * TR_T;
+  const bf16_t* s = src + (size_t)z * R * C;
+  bf16_t* d = dst + (size_t)z * R * C;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < TR_T; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    t[i][tx] = (r < R && c < C) ? s[(size_t)r * C + c] : (bf16_t)0;
+  }
+  __syncthreads();
+  for (int i = ty; i < TR_T; i += 4) {
+    const int c = c0 + i, r = r0 + tx;
+    if (c < C && r < R) d[(size_t)c * R + r] = t[tx][i];
+  }
+}
+
+// Polar Express coefficients (muon.py:19-25; num_iters 5, safety 2e-2, cushion 2).
+constexpr double PE_COEF[5][3] = {
+    {8.156554524902461, -22.48329292557795, 15.878769915207462},
+    {4.042929935166739, -2.808917465908714, 0.5000178451051316},
+    {3.8916678022926607, -2.772484153217685, 0.5060648178503393},
+    {3.285753657755655, -2.3681294933425376, 0.46449024233003106},
+    {2.3465413258596377, -1.7097828382687081, 0.42323551169305323},
+};
+
+namespace {
+// The eager bf16 ops of the reference multiply by a Python float, which a
+// bf16 array takes in its own dtype: the coefficient enters as bf16.
+float bf16_round_host(double v) {
+  float f = (float)v;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
+size_t up256(size_t v) { return (v + 255) / 256 * 256; }
+}  // namespace
+
+size_t polar_express_ws_bytes(int batch, int M, int N) {
+  if (batch <= 0 || M <= 0 || N <= 0) return 0;
+  const size_t mn = (size_t)M * N, S = M < N ? M : N;
+  const size_t nch = (mn + PE_CHUNK - 1) / PE_CHUNK;
+  return up256(batch * mn * 2) * 2 + up256(batch * S * S * 2) * 2 + up256(batch * nch * 4);
+}
+
+hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, void* ws,
+                         size_t ws_bytes, hipStream_t st) {
+  if (batch <= 0 || batch > 65535 || M <= 0 || N <= 0 || M % 64 || N % 64 || !g || !out ||
+      !ws || ws_bytes < polar_express_ws_bytes(batch, M, N))
+    return hipErrorInvalidValue;
+  const size_t mn = (size_t)M * N, S = M < N ? M : N;
+  const int nch = (int)((mn + PE_CHUNK - 1) / PE_CHUNK);
+  char* w = (char*)ws;
+  bf16_t* xb = (bf16_t*)w;  w += up256(batch * mn * 2);    // the other x buffer
+  bf16_t* xt = (bf16_t*)w;  w += up256(batch * mn * 2);    // x^T
+  bf16_t* am = (bf16_t*)w;  w += up256(batch * S * S * 2); // A
+  bf16_t* bm = (bf16_t*)w;  w += up256(batch * S * S * 2); // B
+  float* part = (float*)w;
+  // x0 goes to xb so that the fifth (odd) iteration lands in out
+  hipLaunchKernelGGL(k_pe_sumsq, dim3(nch, batch), dim3(PE_THREADS), 0, st, g, mn, nch, part);
+  hipLaunchKernelGGL(k_pe_scale, dim3(grid_for(mn, 256) < 4096 ? grid_for(mn, 256) : 4096, batch),
+                     dim3(256), 0, st, g, mn, nch, part, xb);
+  bf16_t* cur = xb;
+  bf16_t* nxt = out;
+  const bool tall = M > N;
+  const dim3 tg((N + TR_T - 1) / TR_T, (M + TR_T - 1) / TR_T, batch);
+  for (int it = 0; it < 5; ++it) {
+    const float a = bf16_round_host(PE_COEF[it][0]);
+    const float b = bf16_round_host(PE_COEF[it][1]);
+    const float c = bf16_round_host(PE_COEF[it][2]);
+    EpiArgs ea{};
+    hipError_t e;
+    hipLaunchKernelGGL(k_transpose_bf16, tg, dim3(256), 0, st, cur, xt, M, N);
+    if (!tall) {
+      // A = x x^T (M x M, K = N)
+      ea.out = am;
+      ea.ldo = M;
+      e = gemm_batched(EPI_STORE, cur, N, (long long)mn, cur, (long long)mn, M, M, N, ea,
+                       (long long)S * S, 0, batch, st);
+      if (e != hipSuccess) return e;
+      // B = b A + c (A A)
+      ea.out = bm;
+      ea.x = am;
+      ea.ldr = M;
+      ea.s0 = b;
+      ea.s1 = c;
+      e = gemm_batched(EPI_PE_B, am, M, (long long)S * S, am, (long long)S * S, M, M, M, ea,
+                       (long long)S * S, (long long)S * S, batch, st);
+      if (e != hipSuccess) return e;
+      // x' = a x + B x: B (M x M) against x^T (N x M)
+      ea.out = nxt;
+      ea.ldo = N;
+      ea.x = cur;
+      ea.ldr = N;
+      ea.s0 = a;
+      e = gemm_batched(EPI_PE_X, bm, M, (long long)S * S, xt, (long long)mn, M, N, M, ea,
+                       (long long)mn, (long long)mn, batch, st);
+      if (e != hipSuccess) return e;
+    } else {
+      // A = x^T x (N x N, K = M) from x^T (N x M)
+      ea.out = am;
+      ea.ldo = N;
+      e = gemm_batched(EPI_STORE, xt, M, (long long)mn, xt, (long long)mn, N, N, M, ea,
+                       (long long)S * S, 0, batch, st);
+      if (e != hipSuccess) return e;
+      ea.out = bm;
+      ea.x = am;
+      ea.ldr = N;
+      ea.s0 = b;
+      ea.s1 = c;
+      e = gemm_batched(EPI_PE_B, am, N, (long long)S * S, am, (long long)S * S, N, N, N, ea,
+                       (long long)S * S, (long long)S * S, batch, st);
+      if (e != hipSuccess) return e;
+      // x' = a x + x B (B symmetric: its rows are the columns of B)
+      ea.out = nxt;
+      ea.ldo = N;
+      ea.x = cur;
+      ea.ldr = N;
+      ea.s0 = a;
+      e = gemm_batched(EPI_PE_X, cur, N, (long long)mn, bm, (long long)S * S, M, N, N, ea,
+                       (long long)mn, (long long)mn, batch, st);
+      if (e != hipSuccess) return e;
+    }
+    bf16_t* t = cur;
+    cur = nxt;
+    nxt = t;
+  }
+  return hipGetLastError();
+}
+
+// ---- NorMuon ------------------------------------------------------------------
+
+// Mean of v^2 along the reduced axis: per row when M >= N (one wave per
+// row), per column otherwise (one thread per column, rows in order).
+__global__ __launch_bounds__(256) void k_nm_mean_rows(const bf16_t* __restrict__ v, int M, int N,
+                                                      float* __restrict__ vm) {
+  const int z = blockIdx.y;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const bf16_t* r = v + ((size_t)z * M + row) * N;
+  float s = 0.f;
+  for (int j = lane; j < N; j += 64) {
+    const float f = bf2f(r[j]);
+    s += f * f;
+  }
+  s = wave_sum(s);
+  if (lane == 0) vm[(size_t)z * M + row] = s / (float)N;
+}
+
+__global__ __launch_bounds__(256) void k_nm_mean_cols(const bf16_t* __restrict__ v, int M, int N,
+                                                      float* __restrict__ vm) {
+  const int z = blockIdx.y;
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= N) return;
+  const bf16_t* c = v + (size_t)z * M * N + col;
+  float s = 0.f;
+  for (int i = 0; i < M; ++i) {
+    const float f = bf2f(c[(size_t)i * N]);
+    s += f * f;
+  }
+  vm[(size_t)z * N + col] = s / (float)M;
+}
+
+// One work-group per matrix: v_norm, the second-moment update, the step
+// sizes and the final per-line scale (muon.py:55-62).
+constexpr int NM_THREADS = 1024;
+__global__ __launch_bounds__(NM_THREADS) void k_nm_scale(const float* __restrict__ vm, int R,
+                                                        int red, float beta2,
+                                                        float* __restrict__ sm,
+                                                        float* __restrict__ scale) {
+  __shared__ float buf[NM_THREADS];
+  const int z = blockIdx.x, tid = threadIdx.x;
+  const float* vz = vm + (size_t)z * R;
+  float* sz = sm + (size_t)z * R;
+  float* cz = scale + (size_t)z * R;
+  auto block_sum = [&](float x) {
+    buf[tid] = x;
+    __syncthreads();
+    for (int w = NM_THREADS / 2; w > 0; w >>= 1) {
+      if (tid < w) buf[tid] += buf[tid + w];
+      __syncthreads();
+    }
+    const float r = buf[0];
+    __syncthreads();
+    return r;
+  };
+  float s = 0.f;
+  for (int i = tid; i < R; i += NM_THREADS) s += vz[i];
+  const float v_norm = sqrtf(block_sum(s) * (float)red);
+  float q = 0.f;
+  for (int i = tid; i < R; i += NM_THREADS) {
+    const float m2 = sz[i] + (1.0f - beta2) * (vz[i] - sz[i]);
+    sz[i] = m2;
+    const float stp = rsqrtf(fmaxf(m2, 1e-10f));
+    cz[i] = stp;
+    q += (vz[i] * (float)red) * (stp * stp);
+  }
+  const float v_norm_new = sqrtf(block_sum(q));
+  const float ratio = v_norm / fmaxf(v_norm_new, 1e-10f);
+  for (int i = tid; i < R; i += NM_THREADS) cz[i] = cz[i] * ratio;
+}
+
+__global__ void k_nm_apply(const bf16_t* __restrict__ v, int M, int N, int rows,
+                           const float* __restrict__ scale, float* __restrict__ out, int batch) {
+  const size_t mn = (size_t)M * N, n = mn * batch;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const size_t z = i / mn, e = i - z * mn;
+    const size_t line = rows ? e / N : e % N;
+    out[i] = bf2f(v[i]) * scale[z * (rows ? M : N) + line];
+  }
+}
+
+size_t normuon_ws_bytes(int batch, int M, int N) {
+  const size_t R = M >= N ? M : N;
+  return batch > 0 ? 2 * up256((size_t)batch * R * 4) : 0;
+}
+
+hipError_t normuon(const bf16_t* v, float* second_mom, int batch, int M, int N, float beta2,
+                   float* out, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (batch <= 0 || M <= 0 || N <= 0 || !v || !second_mom || !out || !ws ||
+      ws_bytes < normuon_ws_bytes(batch, M, N))
+    return hipErrorInvalidValue;
+  const bool rows = M >= N;
+  const int R = rows ? M : N, red = rows ? N : M;
+  float* vm = (float*)ws;
+  float* sc = (float*)((char*)ws + up256((size_t)batch * R * 4));
+  if (rows)
+    hipLaunchKernelGGL(k_nm_mean_rows, dim3((M + 3) / 4, batch), dim3(256), 0, st, v, M, N, vm);
+  else
+    hipLaunchKernelGGL(k_nm_mean_cols, dim3((N + 255) / 256, batch), dim3(256), 0, st, v, M, N,
+                       vm);
+  hipLaunchKernelGGL(k_nm_scale, dim3(batch), dim3(NM_THREADS), 0, st, vm, R, red, beta2,
+                     second_mom, sc);
+  hipLaunchKernelGGL(k_nm_apply, dim3(grid_for((size_t)batch * M * N, 256)), dim3(256), 0, st, v,
+                     M, N, (int)rows, sc, out, batch);
+  return hipGetLastError();
+}
+
+hipError_t adam_step(const float* p, const float* g, const float* m, const float* v, size_t n,
+                     float b1, float b2, float eps, float step, float wd, float* po, float* mo,
+                     float* vo, hipStream_t st) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_adam, dim3(grid_for(n, 256)), dim3(256), 0, st, p, g, m, v, n, b1, b2, eps,
+                     step, wd, po, mo, vo);
+  return hipGetLastError();
+}
+
+hipError_t muon_momentum(const float* g, const float* buf, size_t n, float mu, float* geff,
+                         float* bo, hipStream_t st) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_muon_momentum, dim3(grid_for(n, 256)), dim3(256), 0, st, g, buf, n, mu,
+                     geff, bo);
+  return hipGetLastError();
+}
+
+hipError_t muon_apply(const float* p, const float* u, size_t n, float lr, float wd, float* po,
+                      hipStream_t st) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_muon_apply, dim3(grid_for(n, 256)), dim3(256), 0, st, p, u, n, lr, wd, po);
+  return hipGetLastError();
+}
+
+}  // namespace ann

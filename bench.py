@@ -211,6 +211,56 @@ def secondary_b64(cfg, params):
     }
 
 
+def polar_express_flops(shape):
+    """Five iterations of A = x x^T (or x^T x), A A, B x (or x B) per matrix."""
+    *lead, M, N = shape
+    batch = int(np.prod(lead)) if lead else 1
+    S, L = min(M, N), max(M, N)
+    return 5 * batch * (4 * S * S * L + 2 * S ** 3)
+
+
+def secondary_optim(cfg, params):
+    """One MuonAdam step (muon.py:66-137) over the 155M parameter dict with
+    random gradients; Polar Express timed alone against the MFMA peak."""
+    import torch
+    from attention_nn_amd import optim as G
+    p = {k: torch.from_numpy(v).cuda() for k, v in params.items()}
+    rng = torch.Generator(device="cuda").manual_seed(5)
+    grads = {k: torch.randn(v.shape, device="cuda", generator=rng) * 1e-3 for k, v in p.items()}
+    opt = G.MuonAdam(p, G.optimizer_table())
+    p = opt(p, grads)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    e0.record()
+    for _ in range(reps):
+        p = opt(p, grads)
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / reps
+    banks = [grads[k] for k in ("attn_bank", "fc_bank", "proj_bank")]
+    for g in banks:
+        G.polar_express(g)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for g in banks:
+            G.polar_express(g)
+    e1.record()
+    torch.cuda.synchronize()
+    pe_ms = e0.elapsed_time(e1) / reps
+    pe_fl = sum(polar_express_flops(tuple(g.shape)) for g in banks)
+    tf = pe_fl / (pe_ms / 1e3) / 1e12
+    del p, grads, opt
+    torch.cuda.empty_cache()
+    return {"optimizer_step": {
+        "ms": round(step_ms, 3), "polar_express_ms": round(pe_ms, 3),
+        "polar_express_tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_TFLOPS, 4),
+        "polar_express_flops": pe_fl,
+        "workload": "MuonAdam step over the 155M parameter dict (attn/fc/proj banks on "
+                    "NorMuon + Polar Express, embeddings and lambdas on Adam), random grads"}}
+
+
 def extra_config(name):
     """prefill then decode, reported as secondary lines."""
     import torch
@@ -347,6 +397,7 @@ def main():
 
     if not args.no_secondary:
         sec.update(secondary_b64(cfg, params))
+        sec.update(secondary_optim(cfg, params))
     for name in [c for c in args.configs.split(",") if c]:
         sec[name] = extra_config(name)
     out["secondary"] = sec

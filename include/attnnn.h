@@ -28,6 +28,11 @@
  *   ann_op_rope_ht                            <- rope_ht (metal_kernels.py:87-134)
  *   ann_op_rope_tables                        <- make_rope_tables (metal_kernels.py:144-150)
  *   ann_op_rms_norm                           <- rms (model.py:48-49)
+ *   ann_op_adam_step                          <- adam_step (metal_kernels.py:241-270)
+ *   ann_op_muon_momentum                      <- muon_momentum (metal_kernels.py:277-300)
+ *   ann_op_muon_apply                         <- muon_apply (metal_kernels.py:306-329)
+ *   ann_op_polar_express(_ws_bytes)           <- polar_express (muon.py:28-44)
+ *   ann_op_normuon(_ws_bytes)                 <- normuon_rescale (muon.py:47-63)
  */
 #ifndef ATTNNN_H
 #define ATTNNN_H
@@ -190,6 +195,31 @@ int ann_op_rms_norm(const void* x, void* y, int32_t rows, int32_t dim, float eps
 #define ANN_PROF_STEP 6   /* the persistent batch-1 decode kernel (whole step) */
 int ann_profile_enable(ann_ctx* ctx, int32_t kind, int32_t max_launches);
 int ann_profile_read(ann_ctx* ctx, float* total_ms, int32_t* launches);
+
+/* ---- optimizer step (MuonAdam, muon.py:66-137) ----------------------------
+ * All arrays are device fp32 unless noted; n elements; outputs may alias the
+ * matching inputs.  Scalars as the reference passes them. */
+/* adam_step: m' = b1 m + (1-b1) g; v' = b2 v + (1-b2) g^2;
+ * u = m' / (sqrt(v') + eps) * step_size; u += p * eff_wd where u * p > 0; p' = p - u. */
+int ann_op_adam_step(const float* p, const float* g, const float* m, const float* v, size_t n,
+                     float beta1, float beta2, float eps, float step_size, float eff_wd,
+                     float* p_out, float* m_out, float* v_out, void* stream);
+/* muon_momentum: buf' = buf + (1-mu)(g - buf); geff = g + mu (buf' - g). */
+int ann_op_muon_momentum(const float* g, const float* buf, size_t n, float mu, float* geff,
+                         float* buf_out, void* stream);
+/* muon_apply: p' = p - p*wd*lr (where u*p >= 0) - u*lr. */
+int ann_op_muon_apply(const float* p, const float* u, size_t n, float lr, float wd, float* p_out,
+                      void* stream);
+/* polar_express: g (batch, M, N) fp32 -> out (batch, M, N) bf16, M and N
+ * multiples of 64; ws: ann_op_polar_express_ws_bytes(batch, M, N) bytes. */
+size_t ann_op_polar_express_ws_bytes(int32_t batch, int32_t M, int32_t N);
+int ann_op_polar_express(const float* g, int32_t batch, int32_t M, int32_t N, void* out,
+                         void* ws, size_t ws_bytes, void* stream);
+/* normuon_rescale: v (batch, M, N) bf16; second_mom (batch, M) if M >= N else
+ * (batch, N), updated in place; out (batch, M, N) fp32. */
+size_t ann_op_normuon_ws_bytes(int32_t batch, int32_t M, int32_t N);
+int ann_op_normuon(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
+                   float beta2, float* out, void* ws, size_t ws_bytes, void* stream);
 
 /* Device status of the persistent batch-1 decode step (no reference
  * counterpart).  Its cross-work-group waits are bounded; one that gives up

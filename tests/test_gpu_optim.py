@@ -1,0 +1,105 @@
+"""The optimizer step on the GPU (through the C ABI) against the oracle
+(oracle/ref_optim.py): the reference's kernel self-tests, Polar Express,
+NorMuon and whole MuonAdam steps over a model-shaped parameter dict."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.ref_optim as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import attention_nn_amd._lib as L
+    L.lib()
+
+
+def _cuda(*ts):
+    return [t.cuda() for t in ts]
+
+
+def test_elementwise_kernels_reference_selftests():
+    """metal_kernels.py:373-398 on the HIP kernels, at the reference's atol."""
+    from attention_nn_amd import optim as G
+    from tests.test_optim_oracle import _selftest_inputs
+    p, g, buf, gg = _selftest_inputs()
+    z = torch.zeros(1000)
+    pn, mn, vn = G.adam_step(*_cuda(p, g, z, z), 0.9, 0.99, 1e-10, 0.01, 0.05)
+    rp, rm, rv = O.adam_step(p, g, z, z, 0.9, 0.99, 1e-10, 0.01, 0.05)
+    assert torch.allclose(pn.cpu(), rp, atol=1e-6)
+    assert torch.allclose(mn.cpu(), rm, atol=1e-6) and torch.allclose(vn.cpu(), rv, atol=1e-6)
+    ge, bo = G.muon_momentum(*_cuda(gg, buf), 0.95)
+    rge, rbo = O.muon_momentum(gg, buf, 0.95)
+    assert torch.allclose(ge.cpu(), rge, atol=1e-6) and torch.allclose(bo.cpu(), rbo, atol=1e-6)
+    pa = G.muon_apply(*_cuda(p, g), 0.02, 1.2)
+    assert torch.allclose(pa.cpu(), O.muon_apply(p, g, 0.02, 1.2), atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(3, 64, 64), (2, 64, 256), (2, 256, 64), (1, 768, 3072)])
+def test_polar_express_matches_oracle(shape):
+    """The bf16 iteration is sensitive at the ulp level: one ulp more or less
+    in the Frobenius denominator (a different fp32 summation order) moves the
+    output by 2.1-2.6% relative on the oracle itself, and this is the only
+    difference measured between the kernel and the oracle (0.0% for some
+    shapes, 2.4% for others).  The 4% bound still rejects every plausible
+    mistake, measured on the oracle: a missing normalisation factor 6-12%,
+    four iterations instead of five 40%, a dropped term or transpose
+    diverges."""
+    from attention_nn_amd import optim as G
+    torch.manual_seed(sum(shape))
+    g = torch.randn(shape)
+    print(f"case polar_express {shape}", flush=True)
+    got = G.polar_express(g.cuda()).float().cpu()
+    ref = O.polar_express(g)
+    rel = ((got - ref).norm(dim=(-2, -1)) / ref.norm(dim=(-2, -1))).max().item()
+    assert rel < 4e-2, rel
+    s = torch.linalg.svdvals(got.double())
+    assert s.max().item() < 1.2
+
+
+@pytest.mark.parametrize("shape", [(4, 128, 64), (2, 64, 192)])
+def test_normuon_matches_oracle(shape):
+    from attention_nn_amd import optim as G
+    torch.manual_seed(7)
+    v = torch.randn(shape).bfloat16().float()
+    M, N = shape[-2], shape[-1]
+    red = -1 if M >= N else -2
+    sm = torch.rand([s if i != len(shape) + red else 1 for i, s in enumerate(shape)]) * 0.1
+    out, smn = G.normuon_rescale(v.cuda(), sm.cuda(), 0.9)
+    rout, rsm = O.normuon_rescale(v, sm, 0.9)
+    assert torch.allclose(smn.cpu().reshape(rsm.shape), rsm, rtol=1e-5, atol=1e-8)
+    assert torch.allclose(out.cpu(), rout, rtol=1e-4, atol=1e-6)
+
+
+def test_muon_adam_steps_match_oracle():
+    """Three MuonAdam steps over a small model's parameter dict (every rule
+    of the table: muon banks, square and tall and wide, Adam embeddings and
+    lambdas), schedules changing between steps."""
+    from attention_nn_amd import optim as G
+    from attention_nn_amd.config import GPTConfig
+    from attention_nn_amd.weights import init_params
+    cfg = GPTConfig(vocab_size=192, num_layers=2, num_heads=2, model_dim=64, seq_len=32,
+                    window=16, long_layers=(1,))
+    p0 = {k: torch.from_numpy(v) for k, v in init_params(cfg, 3, dense=True).items()}
+    table = O.optimizer_table()
+    ref = O.MuonAdam(p0, table)
+    gpu = G.MuonAdam({k: v.cuda() for k, v in p0.items()}, G.optimizer_table())
+    pr = dict(p0)
+    pg = {k: v.cuda() for k, v in p0.items()}
+    rng = np.random.default_rng(11)
+    for step, (lr_s, mom) in enumerate([(1.0, 0.85), (0.7, 0.9), (0.4, 0.95)]):
+        grads = {k: torch.from_numpy(rng.standard_normal(v.shape).astype(np.float32) * 0.01)
+                 for k, v in p0.items()}
+        pr = ref(pr, grads, lr_s, mom)
+        pg = gpu(pg, {k: v.cuda() for k, v in grads.items()}, lr_s, mom)
+        for k in p0:
+            d = (pg[k].cpu() - pr[k]).abs().max().item()
+            scale = (pr[k] - p0[k]).abs().max().item() + 1e-12
+            # the update is what the step computes: compare against its size
+            assert d <= 0.05 * scale + 1e-7, (step, k, d, scale)
+    assert float(gpu.state["_step"]["t"].item()) == 3.0
