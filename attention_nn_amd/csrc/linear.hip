@@ -442,38 +442,47 @@ __device__ __forceinline__ void qkv_tile_epilogue(const EpiArgs& ea, const bf16_
 
 // BM = 128 for prefill; BM = 64 when M <= 64 (no padding rows in the MFMAs:
 // the batch-64 lm_head runs 1.4x faster measured).
-template <int EPI, int BM>
+template <int EPI, int BM, int BN>
 __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
                                           const bf16_t* __restrict__ W, int M, int N, int K,
                                           const EpiArgs& ea) {
   constexpr int AC = BM * GM_BK / 8 / 256;   // 16-byte A chunks per thread per K tile
+  constexpr int BC = BN * GM_BK / 8 / 256;   // and of W
   constexpr int WM = BM / 2, MT = WM / 16;   // rows per wave, 16-row MFMA tiles per wave
-  __shared__ __attribute__((aligned(16))) bf16_t smem[(BM + GM_BN) * GM_LDS];
+  constexpr int WN = BN / 2, NT = WN / 16;   // columns per wave, 16-column tiles per wave
+  constexpr int CH = AC > BC ? AC : BC;
+  // the QKV and CE epilogues work on 128-column tiles (whole heads; the
+  // per-tile partial sums of the loss)
+  static_assert((EPI != EPI_QKV && EPI != EPI_CE) || BN == GM_BN, "128-column tiles");
+  constexpr int SMEM = (BM + BN) * GM_LDS > (EPI == EPI_QKV ? BM * (GM_BN + 8) : 0)
+                           ? (BM + BN) * GM_LDS
+                           : BM * (GM_BN + 8);
+  __shared__ __attribute__((aligned(16))) bf16_t smem[SMEM];
   bf16_t* As = smem;
   bf16_t* Bs = smem + BM * GM_LDS;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv >> 1, wn = wv & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * GM_BN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  // each thread moves AC 16-byte chunks of A and 4 of B per K tile
-  int arow[4], acol[4];
-  bool aok[4], bok[4];
+  // each thread moves AC 16-byte chunks of A and BC of W per K tile
+  int arow[CH], acol[CH];
+  bool aok[CH], bok[CH];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < CH; ++i) {
     const int id = tid + i * 256;
     arow[i] = id >> 3;
     acol[i] = (id & 7) * 8;
     aok[i] = i < AC && (m0 + arow[i]) < M;
-    bok[i] = (n0 + arow[i]) < N;
+    bok[i] = i < BC && (n0 + arow[i]) < N;
   }
-  uint4 ra[AC], rb[4];
+  uint4 ra[AC], rb[BC];
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < AC; ++i)
       ra[i] = aok[i] ? *(const uint4*)(A + (size_t)(m0 + arow[i]) * lda + k0 + acol[i])
                      : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < BC; ++i)
       rb[i] = bok[i] ? *(const uint4*)(W + (size_t)(n0 + arow[i]) * K + k0 + acol[i])
                      : make_uint4(0, 0, 0, 0);
   };
@@ -481,7 +490,7 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
 #pragma unroll
     for (int i = 0; i < AC; ++i) *(uint4*)(As + arow[i] * GM_LDS + acol[i]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(uint4*)(Bs + arow[i] * GM_LDS + acol[i]) = rb[i];
+    for (int i = 0; i < BC; ++i) *(uint4*)(Bs + arow[i] * GM_LDS + acol[i]) = rb[i];
   };
 
   // SWAP: acc[j][i] is block (N block j, M block i) of C^T = W A^T, so that a
@@ -491,9 +500,9 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   // epilogues gain from SWAP (prefill o / proj 20 us each), the plain stores
   // lose (qkv / fc 16 us each).
   constexpr bool SWAP = EPI != EPI_STORE && EPI != EPI_RELU2;
-  floatx4_t acc[4][MT];
+  floatx4_t acc[NT][MT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < NT; ++j)
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[j][i] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
 
@@ -506,16 +515,16 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
     if (k0 + GM_BK < K) load_tile(k0 + GM_BK);
 #pragma unroll
     for (int kk = 0; kk < GM_BK; kk += 32) {
-      bf16x8_t a[MT], b[4];
+      bf16x8_t a[MT], b[NT];
 #pragma unroll
       for (int i = 0; i < MT; ++i)
         a[i] = *(const bf16x8_t*)(As + (wm * WM + i * 16 + r16) * GM_LDS + kk + kq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *(const bf16x8_t*)(Bs + (wn * 64 + j * 16 + r16) * GM_LDS + kk + kq);
+      for (int j = 0; j < NT; ++j)
+        b[j] = *(const bf16x8_t*)(Bs + (wn * WN + j * 16 + r16) * GM_LDS + kk + kq);
       if constexpr (SWAP) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int i = 0; i < MT; ++i)
             acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a[i], acc[j][i], 0, 0, 0);
@@ -523,7 +532,7 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < NT; ++j)
             acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
       }
     }
@@ -533,8 +542,8 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + r16;
+      for (int j = 0; j < NT; ++j) {
+        const int n = n0 + wn * WN + j * 16 + r16;
         if (n >= N) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -557,10 +566,10 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
       const int tg = m < M ? ea.tgt[m] : -1;
       float sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int n = n0 + wn * 64 + j * 16 + (lane >> 4) * 4 + r;
+          const int n = n0 + wn * WN + j * 16 + (lane >> 4) * 4 + r;
           if (n < N) {
             const float zc = softcap(bf2f(f2bf(acc[j][i][r])));
             sum += __expf(zc);
@@ -587,13 +596,13 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
     }
   } else if constexpr (EPI == EPI_QKV) {
     __syncthreads();   // every wave is done with the last K tile in LDS
-    constexpr int CP = GM_BN + 8;
+    constexpr int CP = BN + 8;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const floatx4_t y = acc[j][i];
-        *(uint2*)(smem + (wm * WM + i * 16 + r16) * CP + wn * 64 + j * 16 + (lane >> 4) * 4) =
+        *(uint2*)(smem + (wm * WM + i * 16 + r16) * CP + wn * WN + j * 16 + (lane >> 4) * 4) =
             make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     __syncthreads();
@@ -601,8 +610,8 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   } else {
     const bool vec = epi_vec_ok<EPI>(ea);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 64 + j * 16 + (lane >> 4) * 4;
+    for (int j = 0; j < NT; ++j) {
+      const int n = n0 + wn * WN + j * 16 + (lane >> 4) * 4;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = m0 + wm * WM + i * 16 + r16;
@@ -612,11 +621,23 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   }
 }
 
-template <int EPI, int BM>
+template <int EPI, int BM, int BN>
 __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int lda,
                                               const bf16_t* __restrict__ W, int M, int N, int K,
                                               EpiArgs ea) {
-  gemm_body<EPI, BM>(A, lda, W, M, N, K, ea);
+  gemm_body<EPI, BM, BN>(A, lda, W, M, N, K, ea);
+}
+
+// The 256 x 128 and 128 x 256 tiles (waves of 128 x 64 / 64 x 128: a quarter
+// less LDS traffic per flop than 64 x 64) held to two waves per SIMD, so two
+// work-groups share a CU.  Measured 10-15% faster than 128 x 128 on the
+// prefill shapes; without the register cap the compiler takes one wave per
+// SIMD and they are slower.
+template <int EPI, int BM, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_2w(
+    const bf16_t* __restrict__ A, int lda, const bf16_t* __restrict__ W, int M, int N, int K,
+    EpiArgs ea) {
+  gemm_body<EPI, BM, BN>(A, lda, W, M, N, K, ea);
 }
 
 // Batched: blockIdx.z selects matrix z; A, W, the output and the epilogue's
@@ -629,7 +650,7 @@ __global__ __launch_bounds__(256) void k_gemm_bat(const bf16_t* __restrict__ A, 
   const long long z = blockIdx.z;
   ea.out += z * sOut;
   ea.x += z * sX;
-  gemm_body<EPI, BM>(A + z * sA, lda, W + z * sW, M, N, K, ea);
+  gemm_body<EPI, BM, GM_BN>(A + z * sA, lda, W + z * sW, M, N, K, ea);
 }
 
 // ---- skinny MFMA GEMM (decode, M <= 128) ------------------------------------
@@ -854,13 +875,27 @@ bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea) {
 hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                 const EpiArgs& ea, hipStream_t st) {
   if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
-  const int bm = M <= 64 ? 64 : GM_BM;
-  dim3 grid((N + GM_BN - 1) / GM_BN, (M + bm - 1) / bm);
-#define ANN_GM(E)                                                                            \
-  if (bm == 64)                                                                              \
-    hipLaunchKernelGGL((k_gemm<E, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);    \
-  else                                                                                       \
-    hipLaunchKernelGGL((k_gemm<E, GM_BM>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+  // tile: 64 x 128 for at most 64 rows; 128 x 128 below 512 rows; then
+  // 256 x 128 (wide outputs, and the 128-column QKV / CE epilogues) or
+  // 128 x 256 (outputs of at most 1024 columns: the o / proj projections)
+  const int shape = M <= 64 ? 0 : M < 512 ? 1
+                  : (epi == EPI_QKV || epi == EPI_CE || N > 1024) ? 2 : 3;
+  const int bm = shape == 0 ? 64 : shape == 2 ? 256 : 128;
+  const int bn = shape == 3 ? 256 : GM_BN;
+  dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm);
+#define ANN_GM_ONE(E, S)                                                                       \
+  if (S == 0)                                                                                  \
+    hipLaunchKernelGGL((k_gemm<E, 64, GM_BN>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+  else if (S == 1)                                                                             \
+    hipLaunchKernelGGL((k_gemm<E, 128, GM_BN>), grid, dim3(256), 0, st, A, lda, W, M, N, K,    \
+                       ea);                                                                    \
+  else if (S == 2)                                                                             \
+    hipLaunchKernelGGL((k_gemm_2w<E, 256, GM_BN>), grid, dim3(256), 0, st, A, lda, W, M, N, K, \
+                       ea);
+#define ANN_GM(E)                                                                              \
+  ANN_GM_ONE(E, shape)                                                                         \
+  else hipLaunchKernelGGL((k_gemm_2w<E, 128, 256>), grid, dim3(256), 0, st, A, lda, W, M, N,   \
+                          K, ea);                                                              \
   break;
   switch (epi) {
     case EPI_STORE: ANN_GM(EPI_STORE)
@@ -870,14 +905,17 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
     case EPI_LOGITS: ANN_GM(EPI_LOGITS)
     case EPI_QKV:
       if (!gemm_qkv_fits(M, N, K, ea)) return hipErrorInvalidValue;
-      ANN_GM(EPI_QKV)
+      ANN_GM_ONE(EPI_QKV, shape)
+      break;
     case EPI_CE:
       if (!ea.ce_part || !ea.ce_tz || !ea.tgt || ea.ldz < M) return hipErrorInvalidValue;
-      ANN_GM(EPI_CE)
+      ANN_GM_ONE(EPI_CE, shape)
+      break;
     default:
       return hipErrorInvalidValue;
   }
 #undef ANN_GM
+#undef ANN_GM_ONE
   return hipGetLastError();
 }
 
