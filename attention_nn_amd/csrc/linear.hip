@@ -785,6 +785,125 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
     }
 }
 
+// ---- skinny MFMA GEMM, LDS-staged (decode, M <= 128, no RMS prologue) ------
+//
+// Same work split as k_gemm_sk (one 16T x 16T tile per work-group, the four
+// waves split K into quarters), but each wave brings its quarter of the A and
+// W tiles in with contiguous 16-byte loads -- lanes along a row, not the
+// 16-row x 64-byte MFMA fragment pattern, which moves ~3x fewer bytes per CU
+// cycle -- into its own padded LDS region, in rounds of KC k-steps, and reads
+// the fragments back with ds_read_b128.  A wave touches only its own region,
+// so no barrier is needed until the cross-wave sum, whose partials go into
+// each wave's own (then finished) region.  Operands are swapped for the
+// read-modify-write epilogues (8-byte accesses), as in k_gemm.  Bit-identical
+// to k_gemm_sk (same k order per wave, same wave order).
+template <int EPI, int KC, int T>
+__global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, int lda,
+                                                  const bf16_t* __restrict__ W, int M, int N,
+                                                  int K, EpiArgs ea) {
+  constexpr int R = 16 * T;        // rows per operand tile
+  constexpr int CPR = 4 * KC;      // 16-byte chunks per row per round
+  constexpr int PITCH = CPR + 1;   // padded row pitch, in uint4
+  constexpr int NL = R * CPR / 64; // loads per lane per operand per round
+  constexpr int REGION = 2 * R * PITCH;
+  static_assert(REGION * 16 >= T * T * 64 * 16, "partials fit a wave's region");
+  constexpr bool SWAP = EPI != EPI_STORE && EPI != EPI_RELU2;
+  __shared__ uint4 s_t[4][REGION];
+  const int tid = threadIdx.x, lane = tid & 63, wk = tid >> 6;
+  const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16 * T;
+  const int kw = K >> 7;            // k-steps of 32 per wave
+  const int kbase = wk * kw * 32;   // first k of this wave's quarter
+  uint4* sa = s_t[wk];
+  uint4* sw = s_t[wk] + R * PITCH;
+  floatx4_t acc[T][T];
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, q4 = lane >> 4;
+  for (int s0 = 0; s0 < kw; s0 += KC) {
+    uint4 ca[NL], cw[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = 64 * i + lane;
+      const int row = c / CPR, col = c % CPR;
+      const bool ok = s0 + col / 4 < kw;
+      const int am = m0 + row, wn = n0 + row;
+      const size_t ke = (size_t)kbase + (size_t)s0 * 32 + col * 8;
+      ca[i] = (ok && am < M) ? *(const uint4*)(A + (size_t)am * lda + ke) : make_uint4(0, 0, 0, 0);
+      cw[i] = (ok && wn < N) ? *(const uint4*)(W + (size_t)wn * K + ke) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int c = 64 * i + lane;
+      const int row = c / CPR, col = c % CPR;
+      sa[row * PITCH + col] = ca[i];
+      sw[row * PITCH + col] = cw[i];
+    }
+    // LDS accesses of one wave complete in order: its reads below see its
+    // writes above; this keeps the compiler from reordering them
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s0 + s < kw) {
+        uint4 a[T], w[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          a[t] = sa[(16 * t + r16) * PITCH + 4 * s + q4];
+          w[t] = sw[(16 * t + r16) * PITCH + 4 * s + q4];
+        }
+#pragma unroll
+        for (int ta = 0; ta < T; ++ta)
+#pragma unroll
+          for (int tw = 0; tw < T; ++tw)
+            acc[ta][tw] = SWAP ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                     *(bf16x8_t*)&w[tw], *(bf16x8_t*)&a[ta], acc[ta][tw], 0, 0, 0)
+                               : __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                     *(bf16x8_t*)&a[ta], *(bf16x8_t*)&w[tw], acc[ta][tw], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  }
+  // partials of waves 1..3 into their own regions, summed by wave 0 in order
+  floatx4_t* red = (floatx4_t*)s_t[wk];
+  if (wk > 0) {
+#pragma unroll
+    for (int ta = 0; ta < T; ++ta)
+#pragma unroll
+      for (int tw = 0; tw < T; ++tw) red[(ta * T + tw) * 64 + lane] = acc[ta][tw];
+  }
+  __syncthreads();
+  if (wk > 0) return;
+  const bool vec = SWAP && epi_vec_ok<EPI>(ea);
+#pragma unroll
+  for (int ta = 0; ta < T; ++ta)
+#pragma unroll
+    for (int tw = 0; tw < T; ++tw) {
+      floatx4_t v = acc[ta][tw];
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        const floatx4_t p = ((const floatx4_t*)s_t[j])[(ta * T + tw) * 64 + lane];
+        v[0] += p[0];
+        v[1] += p[1];
+        v[2] += p[2];
+        v[3] += p[3];
+      }
+      if (SWAP) {   // lane: row m = r16 of block ta, columns 4 q4 .. +3 of block tw
+        const int m = m0 + 16 * ta + r16;
+        if (m < M) epilogue4<EPI>(ea, vec, m, n0 + 16 * tw + 4 * q4, N, v);
+      } else {
+        const int n = n0 + 16 * tw + r16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * ta + 4 * q4 + r;
+          if (m < M && n < N) epilogue<EPI>(ea, m, n, v[r]);
+        }
+      }
+    }
+}
+
 bool gemm_skinny_fits(int M, int N, int K, bool rms) {
   return M > 0 && M <= 128 && N > 0 && K % 128 == 0 &&
          (!rms || K / 128 <= (M > 32 ? 12 : SK_KB));
@@ -801,6 +920,29 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
   // batch depth: the wave's whole K quarter when it fits (fewer registers ->
   // more resident work-groups)
   const int kw = K >> 7;
+  if (!rms) {
+    // LDS-staged variant: rounds of 8 k-steps (16 x 16 tiles) or 4 (32 x 32)
+#define ANN_SK2(E)                                                                               \
+  if (T == 1) {                                                                                  \
+    if (kw <= 6)                                                                                 \
+      hipLaunchKernelGGL((k_gemm_sk2<E, 6, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_gemm_sk2<E, 8, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+  } else {                                                                                       \
+    hipLaunchKernelGGL((k_gemm_sk2<E, 4, 2>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);   \
+  }                                                                                              \
+  break;
+    switch (epi) {
+      case EPI_STORE: ANN_SK2(EPI_STORE)
+      case EPI_RELU2: ANN_SK2(EPI_RELU2)
+      case EPI_RESID_ATTN: ANN_SK2(EPI_RESID_ATTN)
+      case EPI_RESID_MLP: ANN_SK2(EPI_RESID_MLP)
+      case EPI_LOGITS: ANN_SK2(EPI_LOGITS)
+      default: return hipErrorInvalidValue;
+    }
+#undef ANN_SK2
+    return hipGetLastError();
+  }
   const int kb = kw <= 6 ? 6 : kw <= 12 ? 12 : SK_KB;
 #define ANN_SK_T(E, R, KBV)                                                                   \
   if (T == 1)                                                                                 \
