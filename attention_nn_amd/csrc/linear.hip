@@ -797,10 +797,16 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
 // each wave's own (then finished) region.  Operands are swapped for the
 // read-modify-write epilogues (8-byte accesses), as in k_gemm.  Bit-identical
 // to k_gemm_sk (same k order per wave, same wave order).
-template <int EPI, int KC, int T>
+// RMS: the rows of A are normalised in the kernel (model.py:48-49 with the
+// bf16 output of an eager op): before the first round each wave reads its K
+// quarter of the tile's A rows with contiguous loads, leaves per-chunk sums of
+// squares in its own (not yet used) LDS region, sums each row's chunks in
+// order and the quarters are added in wave order; the fragments are then
+// scaled and rounded to bf16 as they come out of LDS.
+template <int EPI, bool RMS, int KC, int T>
 __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, int lda,
                                                   const bf16_t* __restrict__ W, int M, int N,
-                                                  int K, EpiArgs ea) {
+                                                  int K, float eps, EpiArgs ea) {
   constexpr int R = 16 * T;        // rows per operand tile
   constexpr int CPR = 4 * KC;      // 16-byte chunks per row per round
   constexpr int PITCH = CPR + 1;   // padded row pitch, in uint4
@@ -809,6 +815,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
   static_assert(REGION * 16 >= T * T * 64 * 16, "partials fit a wave's region");
   constexpr bool SWAP = EPI != EPI_STORE && EPI != EPI_RELU2;
   __shared__ uint4 s_t[4][REGION];
+  __shared__ float s_ss[RMS ? 4 : 1][R];
   const int tid = threadIdx.x, lane = tid & 63, wk = tid >> 6;
   const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16 * T;
   const int kw = K >> 7;            // k-steps of 32 per wave
@@ -821,6 +828,50 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
 #pragma unroll
     for (int j = 0; j < T; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15, q4 = lane >> 4;
+  float scale[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) scale[t] = 1.f;
+  if (RMS) {   // host guarantees R * 4 kw floats fit the region
+    const int cq = 4 * kw;          // chunks of a row in this quarter
+    float* ps = (float*)s_t[wk];
+    for (int c0 = 0; c0 < R * cq; c0 += 8 * 64) {   // eight loads in flight per lane
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + 64 * u + lane;
+        const int row = c / cq, col = c % cq;
+        v[u] = (c < R * cq && m0 + row < M)
+                   ? *(const uint4*)(A + (size_t)(m0 + row) * lda + kbase + col * 8)
+                   : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + 64 * u + lane;
+        float f[8];
+        unpack8(v[u], f);
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q += f[j] * f[j];
+        if (c < R * cq) ps[c] = q;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    if (lane < R) {
+      float q = 0.f;
+      for (int col = 0; col < cq; ++col) q += ps[lane * cq + col];
+      s_ss[wk][lane] = q;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int r = 16 * t + r16;
+      const float tt = ((s_ss[0][r] + s_ss[1][r]) + s_ss[2][r]) + s_ss[3][r];
+      scale[t] = rsqrtf(tt / (float)K + eps);
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  }
   for (int s0 = 0; s0 < kw; s0 += KC) {
     uint4 ca[NL], cw[NL];
 #pragma unroll
@@ -852,6 +903,14 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
         for (int t = 0; t < T; ++t) {
           a[t] = sa[(16 * t + r16) * PITCH + 4 * s + q4];
           w[t] = sw[(16 * t + r16) * PITCH + 4 * s + q4];
+          if (RMS) {
+            float f[8];
+            unpack8(a[t], f);
+            a[t] = make_uint4(pack2(f[0] * scale[t], f[1] * scale[t]),
+                              pack2(f[2] * scale[t], f[3] * scale[t]),
+                              pack2(f[4] * scale[t], f[5] * scale[t]),
+                              pack2(f[6] * scale[t], f[7] * scale[t]));
+          }
         }
 #pragma unroll
         for (int ta = 0; ta < T; ++ta)
@@ -904,6 +963,12 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
     }
 }
 
+// Bytes of one wave's LDS region in k_gemm_sk2 (rounds of 6 or 8 k-steps for
+// T = 1 take the larger, 8; T = 2 uses 4).
+constexpr int sk2_region_bytes(int T) {
+  return T == 1 ? 2 * 16 * (4 * 8 + 1) * 16 : 2 * 32 * (4 * 4 + 1) * 16;
+}
+
 bool gemm_skinny_fits(int M, int N, int K, bool rms) {
   return M > 0 && M <= 128 && N > 0 && K % 128 == 0 &&
          (!rms || K / 128 <= (M > 32 ? 12 : SK_KB));
@@ -920,17 +985,29 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
   // batch depth: the wave's whole K quarter when it fits (fewer registers ->
   // more resident work-groups)
   const int kw = K >> 7;
-  if (!rms) {
-    // LDS-staged variant: rounds of 8 k-steps (16 x 16 tiles) or 4 (32 x 32)
-#define ANN_SK2(E)                                                                               \
+  // LDS-staged variant: rounds of 8 k-steps (16 x 16 tiles) or 4 (32 x 32).
+  // With RMS its extra pass over A pays only above 64 rows (measured: cfg5
+  // +1.6%, batch 64 -8.5%, batch 16 -4%), and the row sums of squares of a
+  // quarter must fit a wave's region.
+  if (!rms || (M > 64 && 16 * T * 4 * kw * 4 <= sk2_region_bytes(T))) {
+#define ANN_SK2_R(E, R)                                                                          \
   if (T == 1) {                                                                                  \
     if (kw <= 6)                                                                                 \
-      hipLaunchKernelGGL((k_gemm_sk2<E, 6, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+      hipLaunchKernelGGL((k_gemm_sk2<E, R, 6, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,   \
+                         eps, ea);                                                               \
     else                                                                                         \
-      hipLaunchKernelGGL((k_gemm_sk2<E, 8, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea); \
+      hipLaunchKernelGGL((k_gemm_sk2<E, R, 8, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,   \
+                         eps, ea);                                                               \
   } else {                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk2<E, 4, 2>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);   \
-  }                                                                                              \
+    hipLaunchKernelGGL((k_gemm_sk2<E, R, 4, 2>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
+                       eps, ea);                                                                 \
+  }
+#define ANN_SK2(E)       \
+  if (rms) {             \
+    ANN_SK2_R(E, true)   \
+  } else {               \
+    ANN_SK2_R(E, false)  \
+  }                      \
   break;
     switch (epi) {
       case EPI_STORE: ANN_SK2(EPI_STORE)
@@ -941,6 +1018,7 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
       default: return hipErrorInvalidValue;
     }
 #undef ANN_SK2
+#undef ANN_SK2_R
     return hipGetLastError();
   }
   const int kb = kw <= 6 ? 6 : kw <= 12 ? 12 : SK_KB;
