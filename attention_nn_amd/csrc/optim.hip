@@ -82,18 +82,27 @@ __global__ void k_muon_apply(const float* __restrict__ p, const float* __restric
 
 // ---- Polar Express ------------------------------------------------------------
 
-constexpr int PE_CHUNK = 65536;   // elements per partial sum of squares
-constexpr int PE_THREADS = 256;
+constexpr int PE_CHUNK = 8192;   // elements per partial sum of squares
+constexpr int PE_THREADS = 256;   // a thread reads 8 float4 of a chunk
 
-// Partial sums of squares: block (chunk c, matrix z) over its PE_CHUNK elements.
+// Partial sums of squares: block (chunk c, matrix z), eight independent
+// 16-byte loads per thread, then a fixed-order tree.  mn % 4 == 0 (M, N are
+// multiples of 64).
 __global__ __launch_bounds__(PE_THREADS) void k_pe_sumsq(const float* __restrict__ g, size_t mn,
                                                          int nch, float* __restrict__ part) {
   __shared__ float red[PE_THREADS];
   const int c = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
-  const float* gz = g + (size_t)z * mn;
-  const size_t e0 = (size_t)c * PE_CHUNK, e1 = min(mn, e0 + PE_CHUNK);
+  const float4* gz = (const float4*)(g + (size_t)z * mn);
+  const size_t q0 = (size_t)c * (PE_CHUNK / 4), q1 = min(mn / 4, q0 + PE_CHUNK / 4);
+  float4 v[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const size_t i = q0 + tid + (size_t)u * PE_THREADS;
+    v[u] = i < q1 ? gz[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   float s = 0.f;
-  for (size_t i = e0 + tid; i < e1; i += PE_THREADS) s += gz[i] * gz[i];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s += ((v[u].x * v[u].x + v[u].y * v[u].y) + v[u].z * v[u].z) + v[u].w * v[u].w;
   red[tid] = s;
   __syncthreads();
   for (int w = PE_THREADS / 2; w > 0; w >>= 1) {
@@ -103,18 +112,29 @@ __global__ __launch_bounds__(PE_THREADS) void k_pe_sumsq(const float* __restrict
   if (tid == 0) part[(size_t)z * nch + c] = red[0];
 }
 
-// x = bf16(g / (sqrt(sum) * 1.02 + 1e-6)), the partials summed in order.
-__global__ void k_pe_scale(const float* __restrict__ g, size_t mn, int nch,
-                           const float* __restrict__ part, bf16_t* __restrict__ x) {
-  const int z = blockIdx.y;
+// den[z] = sqrt(sum of the partials) * 1.02 + 1e-6, one wave per matrix,
+// lane-strided then a fixed-order wave reduction.
+__global__ __launch_bounds__(64) void k_pe_norm(const float* __restrict__ part, int nch,
+                                                float* __restrict__ den) {
+  const int z = blockIdx.x, lane = threadIdx.x;
   float s = 0.f;
-  for (int c = 0; c < nch; ++c) s += part[(size_t)z * nch + c];
-  const float den = sqrtf(s) * 1.02f + 1e-6f;
-  const float* gz = g + (size_t)z * mn;
-  bf16_t* xz = x + (size_t)z * mn;
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride)
-    xz[i] = f2bf(gz[i] / den);
+  for (int c = lane; c < nch; c += 64) s += part[(size_t)z * nch + c];
+  s = wave_sum(s);
+  if (lane == 0) den[z] = sqrtf(s) * 1.02f + 1e-6f;
+}
+
+// x = bf16(g / den), four elements per thread.
+__global__ void k_pe_scale(const float* __restrict__ g, size_t mn, const float* __restrict__ den,
+                           bf16_t* __restrict__ x) {
+  const int z = blockIdx.y;
+  const float dz = den[z];
+  const float4* gz = (const float4*)(g + (size_t)z * mn);
+  uint2* xz = (uint2*)(x + (size_t)z * mn);
+  const size_t n4 = mn / 4, stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const float4 v = gz[i];
+    xz[i] = make_uint2(pack2(v.x / dz, v.y / dz), pack2(v.z / dz, v.w / dz));
+  }
 }
 
 // dst (C, R) = src (R, C)^T per matrix, 64 x 64 tiles through LDS.
@@ -166,7 +186,8 @@ size_t polar_express_ws_bytes(int batch, int M, int N) {
   if (batch <= 0 || M <= 0 || N <= 0) return 0;
   const size_t mn = (size_t)M * N, S = M < N ? M : N;
   const size_t nch = (mn + PE_CHUNK - 1) / PE_CHUNK;
-  return up256(batch * mn * 2) * 2 + up256(batch * S * S * 2) * 2 + up256(batch * nch * 4);
+  return up256(batch * mn * 2) * 2 + up256(batch * S * S * 2) * 2 + up256(batch * nch * 4) +
+         up256(batch * 4);
 }
 
 hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, void* ws,
@@ -181,11 +202,14 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
   bf16_t* xt = (bf16_t*)w;  w += up256(batch * mn * 2);    // x^T
   bf16_t* am = (bf16_t*)w;  w += up256(batch * S * S * 2); // A
   bf16_t* bm = (bf16_t*)w;  w += up256(batch * S * S * 2); // B
-  float* part = (float*)w;
+  float* part = (float*)w;  w += up256(batch * (size_t)nch * 4);
+  float* den = (float*)w;
   // x0 goes to xb so that the fifth (odd) iteration lands in out
   hipLaunchKernelGGL(k_pe_sumsq, dim3(nch, batch), dim3(PE_THREADS), 0, st, g, mn, nch, part);
-  hipLaunchKernelGGL(k_pe_scale, dim3(grid_for(mn, 256) < 4096 ? grid_for(mn, 256) : 4096, batch),
-                     dim3(256), 0, st, g, mn, nch, part, xb);
+  hipLaunchKernelGGL(k_pe_norm, dim3(batch), dim3(64), 0, st, part, nch, den);
+  const unsigned sg = grid_for(mn / 4, 256);
+  hipLaunchKernelGGL(k_pe_scale, dim3(sg < 1024 ? sg : 1024, batch), dim3(256), 0, st, g, mn, den,
+                     xb);
   bf16_t* cur = xb;
   bf16_t* nxt = out;
   const bool tall = M > N;
@@ -273,18 +297,35 @@ __global__ __launch_bounds__(256) void k_nm_mean_rows(const bf16_t* __restrict__
   if (lane == 0) vm[(size_t)z * M + row] = s / (float)N;
 }
 
+// Columns: a work-group per 64-column strip, lane = column; its four waves
+// take rows w, w + 4, ... (one 128-byte row segment per wave load) and their
+// sums are added in wave order.
 __global__ __launch_bounds__(256) void k_nm_mean_cols(const bf16_t* __restrict__ v, int M, int N,
                                                       float* __restrict__ vm) {
-  const int z = blockIdx.y;
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= N) return;
+  __shared__ float q[4][64];
+  const int z = blockIdx.y, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
   const bf16_t* c = v + (size_t)z * M * N + col;
   float s = 0.f;
-  for (int i = 0; i < M; ++i) {
-    const float f = bf2f(c[(size_t)i * N]);
-    s += f * f;
+  if (col < N) {
+    int i = wv;
+    for (; i + 12 < M; i += 16) {   // four rows in flight per lane
+      const float f0 = bf2f(c[(size_t)i * N]), f1 = bf2f(c[(size_t)(i + 4) * N]);
+      const float f2 = bf2f(c[(size_t)(i + 8) * N]), f3 = bf2f(c[(size_t)(i + 12) * N]);
+      s += f0 * f0;
+      s += f1 * f1;
+      s += f2 * f2;
+      s += f3 * f3;
+    }
+    for (; i < M; i += 4) {
+      const float f = bf2f(c[(size_t)i * N]);
+      s += f * f;
+    }
   }
-  vm[(size_t)z * N + col] = s / (float)M;
+  q[wv][lane] = s;
+  __syncthreads();
+  if (wv == 0 && col < N)
+    vm[(size_t)z * N + col] = (((q[0][lane] + q[1][lane]) + q[2][lane]) + q[3][lane]) / (float)M;
 }
 
 // One work-group per matrix: v_norm, the second-moment update, the step
@@ -354,7 +395,7 @@ hipError_t normuon(const bf16_t* v, float* second_mom, int batch, int M, int N, 
   if (rows)
     hipLaunchKernelGGL(k_nm_mean_rows, dim3((M + 3) / 4, batch), dim3(256), 0, st, v, M, N, vm);
   else
-    hipLaunchKernelGGL(k_nm_mean_cols, dim3((N + 255) / 256, batch), dim3(256), 0, st, v, M, N,
+    hipLaunchKernelGGL(k_nm_mean_cols, dim3((N + 63) / 64, batch), dim3(256), 0, st, v, M, N,
                        vm);
   hipLaunchKernelGGL(k_nm_scale, dim3(batch), dim3(NM_THREADS), 0, st, vm, R, red, beta2,
                      second_mom, sc);

@@ -307,6 +307,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-b64", action="store_true",
                     help="run only the batch-64 prefill/decode section (for profiling)")
+    ap.add_argument("--only", type=str, default="", choices=["", "b64", "optim", "cfg4", "cfg5"],
+                    help="run only one secondary section and print its JSON (for profiling)")
     ap.add_argument("--configs", type=str, default="",
                     help="comma list of extra workloads to add as secondary lines: cfg4,cfg5")
     ap.add_argument("--trace-run", action="store_true",
@@ -339,8 +341,14 @@ def main():
     prompt_len = 32
     steps = min(args.steps, 1024 - prompt_len)
     prompt = np.random.default_rng(0).integers(0, 50257, (1, prompt_len))
-    if args.only_b64:
+    if args.only_b64 or args.only == "b64":
         print(json.dumps(secondary_b64(cfg, params)), flush=True)
+        return 0
+    if args.only == "optim":
+        print(json.dumps(secondary_optim(cfg, params)), flush=True)
+        return 0
+    if args.only in ("cfg4", "cfg5"):
+        print(json.dumps({args.only: extra_config(args.only)}, default=float), flush=True)
         return 0
     eng = Engine(cfg, params, max_batch=1, max_ctx=1024, max_tokens=1024)
     if args.trace_run:
