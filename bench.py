@@ -278,13 +278,18 @@ def extra_config(name):
     params = init_params(cfg, seed=0, dense=True)
     eng = Engine(cfg, params, max_batch=B, max_ctx=P + S, max_tokens=B * P)
     pr = np.random.default_rng(3).integers(0, 50257, (B, P))
+    # one untimed prefill first: the first launch of each kernel also loads
+    # its code object (a cold call measured ~15 ms slower at cfg4)
+    eng.prefill(pr, temp, k, 11, 0)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 2
     e0.record()
-    nxt, _ = eng.prefill(pr, temp, k, 11, 0)
+    for _ in range(reps):
+        nxt, _ = eng.prefill(pr, temp, k, 11, 0)
     e1.record()
     torch.cuda.synchronize()
-    pms = e0.elapsed_time(e1)
+    pms = e0.elapsed_time(e1) / reps
     ms, _, _, toks = run_decode(eng, pr, S, 0, temp, k, 11)
     byts = np.mean([step_bytes(cfg, B, P + i) for i in range(S)])
     gbs = byts / (ms / S / 1e3) / 1e9
