@@ -5,8 +5,12 @@
 //    weight stream: groups of LPR lanes walk one weight row with 16-byte
 //    loads, U chunks in flight per lane; the (normalised) activations sit in
 //    LDS as bf16 and are read with broadcast.
-//  * k_gemm: prefill and large-batch decode on MFMA (v_mfma_f32_16x16x32_bf16),
-//    128x128x64 tiles, 4 waves of 64x64, register-prefetched K loop.
+//  * k_gemm_sk / k_gemm_sk2: decode projections for 8 < M <= 128 rows on
+//    MFMA, one 16x16 or 32x32 output tile per work-group, K split over the
+//    four waves.
+//  * k_gemm / k_gemm_2w / k_gemm_bat: prefill, wide outputs and batched
+//    products on MFMA (v_mfma_f32_16x16x32_bf16): 64..256 x 128..256 x 64
+//    tiles of four waves, swizzled LDS, register-prefetched K loop.
 #include "common.h"
 #include "launch.h"
 
@@ -450,8 +454,9 @@ __device__ __forceinline__ void qkv_tile_epilogue(const EpiArgs& ea, const bf16_
   }
 }
 
-// BM = 128 for prefill; BM = 64 when M <= 64 (no padding rows in the MFMAs:
-// the batch-64 lm_head runs 1.4x faster measured).
+// Work-group tile BM x BN, four waves of BM/2 x BN/2.  BM = 64 when M <= 64
+// (no padding rows in the MFMAs: the batch-64 lm_head runs 1.4x faster
+// measured), 128 below 512 rows, 256 x 128 / 128 x 256 above (k_gemm_2w).
 template <int EPI, int BM, int BN>
 __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
                                           const bf16_t* __restrict__ W, int M, int N, int K,
