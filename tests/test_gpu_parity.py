@@ -134,6 +134,25 @@ def test_prefill_logits_every_position_long_prompt(dh, window):
     assert err < LOGIT_TOL, err
 
 
+@pytest.mark.parametrize("d,B,T", [(512, 2, 300), (768, 3, 200)])
+def test_prefill_wide_tiles(d, B, T):
+    """Prefill shapes on the large-tile GEMMs: M = B*T >= 512 rows, not a
+    multiple of the 256-row tile, so the QKV / fc projections run on the
+    256 x 128 tiles and o / proj on the 128 x 256 tiles, each with a ragged
+    last row block and a tile count that is not a multiple of the 8 XCDs;
+    logits at every position against the oracle."""
+    cfg = GPTConfig(vocab_size=1000, num_layers=2, num_heads=d // 128, model_dim=d, seq_len=320,
+                    window=100, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 31, dense=True))
+    tok = np.random.default_rng(d + T).integers(0, cfg.vocab_size, (B, T))
+    print(f"case d={d} B={B} T={T}", flush=True)
+    eng = _engine(cfg, p, B)
+    got = eng.forward_logits(tok).cpu()
+    ref = R.logits(cfg, p, tok)
+    err = (got - ref).abs().max().item()
+    assert err < LOGIT_TOL, err
+
+
 # ---- training forward: GPT.__call__ with the fused softcap CE ---------------
 
 @pytest.mark.parametrize("dh,V,B,T", [(64, 512, 1, 40), (128, 1000, 2, 40), (128, 700, 2, 300)])
