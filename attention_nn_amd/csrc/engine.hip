@@ -245,7 +245,12 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   const bool use_gemv = !gemm_only && gemv_fits(M, K);
   const bool use_sk = !gemm_only && !use_gemv && !proj_is_gemm(M, N, K, pre);
   if (epi == EPI_QKV && (use_gemv || use_sk)) return fail(ANN_E_ARG, "fused QKV needs the MFMA GEMM");
-  if (pre == PRE_RMS && !use_gemv && !use_sk) {   // large GEMM: A normalised once into h
+  // 65-128 rows with an RMS prologue and a plain-store epilogue (qkv, fc):
+  // rms_apply + 64 x 64 MFMA tiles beat the skinny kernel's in-kernel RMS
+  // (cfg5 decode 3.99 -> 3.88 ms per step, measured); up to 64 rows the
+  // skinny kernel stays ahead
+  const bool use_d64 = use_sk && pre == PRE_RMS && M > 64 && (epi == EPI_STORE || epi == EPI_RELU2);
+  if (pre == PRE_RMS && !use_gemv && (!use_sk || use_d64)) {   // A normalised once into h
     if (K > c->c.d) return fail(ANN_E_ARG, "RMS prologue wider than the model dim");
     bf16_t* h = c->sp<bf16_t>(c->sl.hn);
     HIPCHK(rms_apply(X, ldx, h, K, M, K, c->c.rms_eps, st));
@@ -255,6 +260,8 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
   ProfScope ps(c, kind, st);
   if (use_gemv)
     HIPCHK(gemv(epi, pre, W, X, ldx, M, N, K, c->c.rms_eps, ea, st));
+  else if (use_d64)
+    HIPCHK(gemm_decode64(epi, X, ldx, W, M, N, K, ea, st));
   else if (use_sk)
     HIPCHK(gemm_skinny(epi, pre == PRE_RMS, X, ldx, W, M, N, K, c->c.rms_eps, ea, st));
   else

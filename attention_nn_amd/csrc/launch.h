@@ -119,6 +119,8 @@ hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, i
                        float* mean, hipStream_t st);
 hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t* W, int M, int N,
                        int K, float eps, const EpiArgs& ea, hipStream_t st);
+hipError_t gemm_decode64(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                         const EpiArgs& ea, hipStream_t st);
 // MFMA GEMM (prefill): y = A @ W^T with A (M, lda) bf16.
 hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                 const EpiArgs& ea, hipStream_t st);

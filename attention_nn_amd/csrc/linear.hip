@@ -1125,6 +1125,21 @@ bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea) {
          ea.vc && ea.pos && ea.cs && ea.sn;
 }
 
+// Decode projections of 65-128 rows with a plain-store epilogue on 64 x 64
+// MFMA tiles (A already normalised).
+hipError_t gemm_decode64(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                         const EpiArgs& ea, hipStream_t st) {
+  if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
+  dim3 grid((N + 63) / 64, (M + 63) / 64);
+  if (epi == EPI_STORE)
+    hipLaunchKernelGGL((k_gemm<EPI_STORE, 64, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
+  else if (epi == EPI_RELU2)
+    hipLaunchKernelGGL((k_gemm<EPI_RELU2, 64, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                 const EpiArgs& ea, hipStream_t st) {
   if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
