@@ -41,12 +41,49 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(ad_bf16x2, b), c, false);
 }
 
+constexpr int AD_PF_U = 16;   // 16-byte prefetch loads in flight per lane
+constexpr unsigned long long AD_PF_MAGIC = 0x9e3779b97f4a7c15ull;
+
+// Prefetch work-group wg of P: reads its share of n16 16-byte words (lanes
+// consecutive, AD_PF_U loads in flight) and folds them into one word that is
+// stored only if it equals AD_PF_MAGIC.
+__device__ __forceinline__ void weight_prefetch(const uint4* __restrict__ p, size_t n16,
+                                                unsigned wg, unsigned P,
+                                                unsigned long long* __restrict__ sink) {
+  const size_t stride = (size_t)P * AD_THREADS;
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  for (size_t i = (size_t)wg * AD_THREADS + threadIdx.x; i < n16; i += stride * AD_PF_U) {
+    uint4 v[AD_PF_U];
+#pragma unroll
+    for (int u = 0; u < AD_PF_U; ++u) {
+      const size_t j = i + u * stride;
+      v[u] = j < n16 ? p[j] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < AD_PF_U; ++u) {
+      acc.x ^= v[u].x;
+      acc.y ^= v[u].y;
+      acc.z ^= v[u].z;
+      acc.w ^= v[u].w;
+    }
+  }
+  const unsigned long long f = ((unsigned long long)(acc.x ^ acc.z) << 32) | (acc.y ^ acc.w);
+  if (f == AD_PF_MAGIC) *sink = f;
+}
+
 template <int DH>
 __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     const bf16_t* __restrict__ qkv, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
     float* __restrict__ part, unsigned* __restrict__ cnt, bf16_t* __restrict__ out, int H,
-    int max_ctx, int window, int is_long, float scale, float shift, float eps, int nsplit) {
+    int max_ctx, int window, int is_long, float scale, float shift, float eps, int nsplit, int nb,
+    const uint4* __restrict__ pf, size_t pf_n16, unsigned long long* __restrict__ pf_sink) {
+  if ((int)blockIdx.z >= nb) {   // grid.z slices past the batch: weight prefetch only
+    const unsigned P = (gridDim.z - nb) * gridDim.y * gridDim.x;
+    const unsigned wg = ((blockIdx.z - nb) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    weight_prefetch(pf, pf_n16, wg, P, pf_sink);
+    return;
+  }
   constexpr int KU = DH / 32;       // 16-byte K slices per lane per chunk (4 lanes per key)
   constexpr int VL = DH / 8;        // lanes per V row
   constexpr int VP = 64 / VL;       // V rows per pass of the wave
@@ -241,20 +278,24 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
                        const float* cs, const float* sn, float* part, unsigned* cnt, bf16_t* out,
                        int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
-                       float eps, int nsplit, hipStream_t st) {
+                       float eps, int nsplit, const WeightPrefetch& pf, hipStream_t st) {
   if (nsplit < 1 || B <= 0) return hipErrorInvalidValue;
+  const bool pfon = pf.slices > 0 && pf.bytes >= 16 && pf.p && pf.sink;
+  if (pfon && ((uintptr_t)pf.p & 15)) return hipErrorInvalidValue;
   const float shift = scale * (float)Dh * 1.02f;
-  dim3 grid(nsplit, H, B);
+  dim3 grid(nsplit, H, B + (pfon ? pf.slices : 0));
+  const uint4* pfp = pfon ? (const uint4*)pf.p : nullptr;
+  const size_t pfn = pfon ? pf.bytes / 16 : 0;
   switch (Dh) {
     case 64:
       hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
                          part, cnt, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
-                         nsplit);
+                         nsplit, B, pfp, pfn, pf.sink);
       break;
     case 128:
       hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
                          part, cnt, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
-                         nsplit);
+                         nsplit, B, pfp, pfn, pf.sink);
       break;
     default:
       return hipErrorInvalidValue;

@@ -74,8 +74,8 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, acnt, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes, ce,
-      ce_tz, ce_rows, ce_mean, total;
+  size_t pos, sp, steps, amax, acnt, pfsink, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes,
+      ce, ce_tz, ce_rows, ce_mean, total;
 };
 
 // Exchange area of the persistent decode step (batch 1): tagged words of
@@ -108,6 +108,7 @@ SLayout ws_layout(const ann_config& c) {
   s.steps = off; off += up(B * 8);
   s.amax = off; off += up((B <= 8 ? B : 1) * (size_t)gemv_blocks(c.V, c.d) * 8);
   s.acnt = off; off += up(B * c.H * 4);
+  s.pfsink = off; off += up(8);
   s.x = off; off += up(M * d * 2);
   s.x0 = off; off += up(M * d * 2);
   s.qkv = off; off += up(M * 3 * d * 2);
@@ -193,6 +194,10 @@ struct ann_ctx {
   bool pd_env = true;    // ANN_PERSIST=0 disables
   bool pd_coop = false;  // ANN_PERSIST_COOP=1: cooperative launch
   bool pd_clear = true;  // exchange area must be cleared before the next use
+  // decode (batch >= 16): prefetch work-groups per attention launch that read
+  // the next projections' weights ahead; -1 = not read yet, -2 = sized by
+  // bytes, >= 0 = fixed by ANN_PREFETCH_WG
+  int pf_wgs = -1;
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -283,6 +288,25 @@ int dec_splits(const ann_config& g, bool lng, int B) {
   return n < 1 ? 1 : n;
 }
 
+// Prefetch work-groups per decode attention launch at batch B reading
+// `bytes`: only where the attention itself is long enough to hide the extra
+// reads (B >= 16), one work-group per 128 KB, 32..512.  Measured per step:
+// 155M B=64 596 -> 575 us (flat over 48..192 work-groups), B=16 at ctx 8192
+// 540 -> 522 us, 834M B=128 3766 -> 3550 us (48 work-groups: 3995 us, the
+// reads outlast the attention).  ANN_PREFETCH_WG=n fixes the count (0: off).
+int prefetch_wgs(ann_ctx* c, int B, size_t bytes) {
+  if (c->pf_wgs == -1) {
+    const char* e = getenv("ANN_PREFETCH_WG");
+    c->pf_wgs = e ? atoi(e) : -2;
+    if (e && c->pf_wgs < 0) c->pf_wgs = 0;
+    if (c->pf_wgs > 1024) c->pf_wgs = 1024;
+  }
+  if (B < 16) return 0;
+  if (c->pf_wgs >= 0) return c->pf_wgs;
+  const size_t n = bytes >> 17;
+  return n < 32 ? 32 : n > 512 ? 512 : (int)n;
+}
+
 // embed + all layers for M = B*T rows whose positions start at pos[b].
 int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
   const ann_config& g = c->c;
@@ -337,11 +361,23 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
     er.lam = lam + 8 * l;
     if (T == 1) {  // decode: fused QK-norm / RoPE / KV append and split combine
       const int ns = dec_splits(g, lng, B);
+      // while the attention streams the KV cache, extra work-groups read this
+      // layer's o / fc / proj weights and the next layer's qkv (contiguous
+      // from o) so the projections find them in the memory-side cache
+      WeightPrefetch pf;
+      const size_t pfb = c->wl.layer_stride - (l + 1 < g.L ? 0 : c->wl.o);
+      const int pfw = prefetch_wgs(c, B, pfb);
+      if (pfw > 0) {
+        pf.p = c->layer_w(l, c->wl.o);
+        pf.bytes = pfb;
+        pf.slices = (pfw + ns * H - 1) / (ns * H);
+        pf.sink = c->sp<unsigned long long>(c->sl.pfsink);
+      }
       {
         ProfScope ps(c, ANN_PROF_ATTN, st);
         HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part,
                            c->sp<unsigned>(c->sl.acnt), ao, B, H, Dh, g.max_ctx, g.window, lng,
-                           g.attn_scale, g.rms_eps, ns, st));
+                           g.attn_scale, g.rms_eps, ns, pf, st));
       }
       rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d, d,
                 er, st);

@@ -134,13 +134,25 @@ hipError_t attn_prefill(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, con
                         bf16_t* out, int B, int T, int H, int Dh, int max_ctx, int window,
                         bool long_layer, float scale, hipStream_t st);
 
+// Weights read ahead by extra work-groups of a decode attention launch, so
+// that the projections after it find them in the memory-side cache instead
+// of HBM.  slices = extra grid.z slices (each nsplit x H work-groups); 0 = none.
+// sink: one 8-byte word the reads are folded into (written only on a 64-bit
+// match with a fixed constant, so the loads cannot be optimised away).
+struct WeightPrefetch {
+  const void* p = nullptr;   // 16-byte aligned
+  size_t bytes = 0;
+  int slices = 0;
+  unsigned long long* sink = nullptr;
+};
+
 // Decode attention with fused QK-norm / RoPE / KV append (one token per
 // sequence) -> out (B, H*Dh) bf16.  part: split scratch (B, H, nsplit, Dh + 1);
 // cnt: B*H arrival counters, zero between calls.
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
                        const float* cs, const float* sn, float* part, unsigned* cnt, bf16_t* out,
                        int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
-                       float eps, int nsplit, hipStream_t st);
+                       float eps, int nsplit, const WeightPrefetch& pf, hipStream_t st);
 
 // Sampling of B rows of bf16 z (B, ldz) over the first Vs entries with the
 // device-resident parameters; uses and increments steps[b]; advances pos[b]

@@ -325,6 +325,44 @@ def test_decode_wide_batch_skinny_tiles(B):
     assert worst < LOGIT_TOL, worst
 
 
+def test_decode_weight_prefetch_bitwise(monkeypatch):
+    """From 16 rows the decode attention launch carries extra work-groups that
+    read the next projections' weights ahead (this layer's o / fc / proj and
+    the next layer's qkv; the last layer's o / fc / proj).  They change no
+    result: logits are bitwise equal with the prefetch off and on (fixed and
+    byte-sized work-group counts), and within tolerance of the oracle."""
+    cfg = GPTConfig(vocab_size=704, num_layers=3, num_heads=2, model_dim=256, seq_len=32,
+                    window=8, long_layers=(2,))
+    p = perturb_lambdas(init_params(cfg, 45, dense=True))
+    B = 16
+    tok = np.random.default_rng(46).integers(0, cfg.vocab_size, (B, 14))
+
+    def run(pf):
+        if pf is None:
+            monkeypatch.delenv("ANN_PREFETCH_WG", raising=False)
+        else:
+            monkeypatch.setenv("ANN_PREFETCH_WG", str(pf))
+        eng = _engine(cfg, p, B)
+        _, lg = eng.prefill(tok[:, :10], want_logits=True)
+        out = [lg.cpu()]
+        for i in range(10, 13):
+            _, lg = eng.decode(torch.from_numpy(tok[:, i].astype(np.int32)).cuda(),
+                               want_logits=True)
+            out.append(lg.cpu())
+        eng.check_device()
+        return torch.stack(out)
+
+    off, fixed, sized = run(0), run(7), run(None)
+    assert torch.equal(off, fixed) and torch.equal(off, sized)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    ref = [R.forward(prep, tok[:, :10], cache)[:, -1]]
+    for i in range(10, 13):
+        ref.append(R.forward(prep, tok[:, i:i + 1], cache)[:, -1])
+    worst = (sized - torch.stack(ref)).abs().max().item()
+    assert worst < LOGIT_TOL, worst
+
+
 def test_wide_lm_head_64_row_tile():
     """A vocabulary wider than 8 d at 12 rows takes the large-tile MFMA GEMM
     with its 64-row work-group tile for the lm_head."""
