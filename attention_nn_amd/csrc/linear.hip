@@ -11,12 +11,27 @@
 //  * k_gemm / k_gemm_2w / k_gemm_bat: prefill, wide outputs and batched
 //    products on MFMA (v_mfma_f32_16x16x32_bf16): 64..256 x 128..256 x 64
 //    tiles of four waves, swizzled LDS, register-prefetched K loop.
+#include <type_traits>
 #include "common.h"
 #include "launch.h"
 
 namespace ann {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+// register-ring element: a native vector (an array of HIP's uint4 struct that
+// stays live across loop iterations is kept in scratch memory, not registers)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// f(integral_constant<int, I>) for I = I0 .. N-1: register-ring slots indexed
+// by compile-time constants (a loop index, even unrolled, leaves the ring in
+// scratch memory)
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 // Epilogue for one output element (row m, column n) of accumulator y.
@@ -457,7 +472,11 @@ __device__ __forceinline__ void qkv_tile_epilogue(const EpiArgs& ea, const bf16_
 // Work-group tile BM x BN, four waves of BM/2 x BN/2.  BM = 64 when M <= 64
 // (no padding rows in the MFMAs: the batch-64 lm_head runs 1.4x faster
 // measured), 128 below 512 rows, 256 x 128 / 128 x 256 above (k_gemm_2w).
-template <int EPI, int BM, int BN>
+// DEPTH: K tiles in flight per thread (a register ring; 1 = the next tile
+// only).  Each K tile of a thread is one memory round trip after the tile
+// before it is stored: with few work-groups and short K loops (decode) a
+// deeper ring keeps more bytes in flight per CU.
+template <int EPI, int BM, int BN, int DEPTH = 1>
 __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
                                           const bf16_t* __restrict__ W, int M, int N, int K,
                                           const EpiArgs& ea) {
@@ -505,22 +524,42 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
     aok[i] = i < AC && (m0 + arow[i]) < M;
     bok[i] = i < BC && (n0 + arow[i]) < N;
   }
-  uint4 ra[AC], rb[BC];
-  auto load_tile = [&](int k0) {
+  u32x4_t ra[DEPTH][AC], rb[DEPTH][BC];
+  // DEPTH > 1: rows past M / N load the last valid row instead (they feed
+  // only outputs that are never stored), so every load is unconditional and
+  // the compiler can wait on the oldest slot alone (vmcnt(N)) instead of on
+  // every load in flight
+  const bf16_t* pa[AC];
+  const bf16_t* pb[BC];
+#pragma unroll
+  for (int i = 0; i < AC; ++i)
+    pa[i] = A + (size_t)min(m0 + arow[i], M - 1) * lda + acol[i];
+#pragma unroll
+  for (int i = 0; i < BC; ++i) pb[i] = W + (size_t)min(n0 + arow[i], N - 1) * K + acol[i];
+  auto load_tile = [&](auto slc, int k0) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slc)::value;
+    if constexpr (DEPTH > 1) {
+#pragma unroll
+      for (int i = 0; i < AC; ++i) ra[sl][i] = *(const u32x4_t*)(pa[i] + k0);
+#pragma unroll
+      for (int i = 0; i < BC; ++i) rb[sl][i] = *(const u32x4_t*)(pb[i] + k0);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < AC; ++i)
-      ra[i] = aok[i] ? *(const uint4*)(A + (size_t)(m0 + arow[i]) * lda + k0 + acol[i])
-                     : make_uint4(0, 0, 0, 0);
+      ra[sl][i] = aok[i] ? *(const u32x4_t*)(A + (size_t)(m0 + arow[i]) * lda + k0 + acol[i])
+                         : (u32x4_t){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < BC; ++i)
-      rb[i] = bok[i] ? *(const uint4*)(W + (size_t)(n0 + arow[i]) * K + k0 + acol[i])
-                     : make_uint4(0, 0, 0, 0);
+      rb[sl][i] = bok[i] ? *(const u32x4_t*)(W + (size_t)(n0 + arow[i]) * K + k0 + acol[i])
+                         : (u32x4_t){0u, 0u, 0u, 0u};
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](auto slc) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slc)::value;
 #pragma unroll
-    for (int i = 0; i < AC; ++i) *(uint4*)(As + gm_lds(arow[i], acol[i] >> 3)) = ra[i];
+    for (int i = 0; i < AC; ++i) *(u32x4_t*)(As + gm_lds(arow[i], acol[i] >> 3)) = ra[sl][i];
 #pragma unroll
-    for (int i = 0; i < BC; ++i) *(uint4*)(Bs + gm_lds(arow[i], acol[i] >> 3)) = rb[i];
+    for (int i = 0; i < BC; ++i) *(u32x4_t*)(Bs + gm_lds(arow[i], acol[i] >> 3)) = rb[sl][i];
   };
 
   // SWAP: acc[j][i] is block (N block j, M block i) of C^T = W A^T, so that a
@@ -538,12 +577,21 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
 
   // fragment rows are 16-row aligned + r16: slot of chunk c is c ^ ((r16 >> 1) & 7)
   const int r16 = lane & 15, kg = lane >> 4, sw = (r16 >> 1) & 7;
-  load_tile(0);
-  for (int k0 = 0; k0 < K; k0 += GM_BK) {
+  // DEPTH > 1 needs K / GM_BK a multiple of DEPTH (host-checked): no break
+  // and no conditional load in the loop; the last DEPTH refills re-read the
+  // last tile (unused)
+  const int KT = K / GM_BK;
+  static_for<0, DEPTH>([&](auto slc) __attribute__((always_inline)) { load_tile(slc, decltype(slc)::value * GM_BK); });
+  for (int kt0 = 0; kt0 < KT; kt0 += DEPTH)
+  static_for<0, DEPTH>([&](auto slc) __attribute__((always_inline)) {
+    const int kt = kt0 + decltype(slc)::value;
     __syncthreads();
-    store_tile();
+    store_tile(slc);
     __syncthreads();
-    if (k0 + GM_BK < K) load_tile(k0 + GM_BK);
+    if constexpr (DEPTH > 1)
+      load_tile(slc, min(kt + DEPTH, KT - 1) * GM_BK);
+    else if (kt + 1 < KT)
+      load_tile(slc, (kt + 1) * GM_BK);
 #pragma unroll
     for (int kk = 0; kk < GM_BK; kk += 32) {
       bf16x8_t a[MT], b[NT];
@@ -569,7 +617,7 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
             acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
       }
     }
-  }
+  });
   if constexpr (!SWAP) {
     // C layout of the 16x16 MFMA: lane holds column (lane & 15), rows 4 (lane >> 4) + r
 #pragma unroll
@@ -659,6 +707,15 @@ __global__ __launch_bounds__(256) void k_gemm(const bf16_t* __restrict__ A, int 
                                               const bf16_t* __restrict__ W, int M, int N, int K,
                                               EpiArgs ea) {
   gemm_body<EPI, BM, BN>(A, lda, W, M, N, K, ea);
+}
+
+// Decode projections of 65-128 rows (64 x 64 tiles, about 200 work-groups):
+// DEPTH K tiles in flight per thread.
+template <int EPI, int BM, int BN, int DEPTH>
+__global__ __launch_bounds__(256) void k_gemm_deep(const bf16_t* __restrict__ A, int lda,
+                                                   const bf16_t* __restrict__ W, int M, int N,
+                                                   int K, EpiArgs ea) {
+  gemm_body<EPI, BM, BN, DEPTH>(A, lda, W, M, N, K, ea);
 }
 
 // The 256 x 128 and 128 x 256 tiles (waves of 128 x 64 / 64 x 128: a quarter
@@ -836,7 +893,10 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
 // squares in its own (not yet used) LDS region, sums each row's chunks in
 // order and the quarters are added in wave order; the fragments are then
 // scaled and rounded to bf16 as they come out of LDS.
-template <int EPI, bool RMS, int KC, int T>
+// D: rounds in flight per wave (a register ring): round r + D is loaded as
+// soon as round r is in LDS, so a wave waits on memory about once per D
+// rounds instead of once per round.
+template <int EPI, bool RMS, int KC, int T, int D>
 __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, int lda,
                                                   const bf16_t* __restrict__ W, int M, int N,
                                                   int K, float eps, EpiArgs ea) {
@@ -905,32 +965,59 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
   }
-  for (int s0 = 0; s0 < kw; s0 += KC) {
-    uint4 ca[NL], cw[NL];
+  u32x4_t ca[D][NL], cw[D][NL];
+  auto load_round = [&](auto slc, int s0) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slc)::value;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = 64 * i + lane;
       const int row = c / CPR, col = c % CPR;
-      const bool ok = s0 + col / 4 < kw;
-      const int am = m0 + row, wn = n0 + row;
-      const size_t ke = (size_t)kbase + (size_t)s0 * 32 + col * 8;
-      ca[i] = (ok && am < M) ? *(const uint4*)(A + (size_t)am * lda + ke) : make_uint4(0, 0, 0, 0);
-      cw[i] = (ok && wn < N) ? *(const uint4*)(W + (size_t)wn * K + ke) : make_uint4(0, 0, 0, 0);
+      if constexpr (D > 1) {
+        // unconditional loads (clamped rows / k-steps feed only outputs and
+        // k-steps that are never used), so the compiler waits on the oldest
+        // round alone instead of on every load in flight
+        const int am = min(m0 + row, M - 1), wn = min(n0 + row, N - 1);
+        const size_t ke = (size_t)kbase + (size_t)min(s0 + col / 4, kw - 1) * 32 + (col & 3) * 8;
+        ca[sl][i] = *(const u32x4_t*)(A + (size_t)am * lda + ke);
+        cw[sl][i] = *(const u32x4_t*)(W + (size_t)wn * K + ke);
+      } else {
+        const bool ok = s0 + col / 4 < kw;
+        const int am = m0 + row, wn = n0 + row;
+        const size_t ke = (size_t)kbase + (size_t)s0 * 32 + col * 8;
+        ca[sl][i] = (ok && am < M) ? *(const u32x4_t*)(A + (size_t)am * lda + ke)
+                                   : (u32x4_t){0u, 0u, 0u, 0u};
+        cw[sl][i] = (ok && wn < N) ? *(const u32x4_t*)(W + (size_t)wn * K + ke)
+                                   : (u32x4_t){0u, 0u, 0u, 0u};
+      }
     }
+  };
+  // D > 1 needs the round count a multiple of D (host-checked): no break and
+  // no conditional load in the loop; the last D refills re-read the last round
+  const int nrounds = (kw + KC - 1) / KC;
+  static_for<0, D>([&](auto slc) __attribute__((always_inline)) { load_round(slc, decltype(slc)::value * KC); });
+  for (int r0 = 0; r0 < nrounds; r0 += D)
+  static_for<0, D>([&](auto slc) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slc)::value;
+    const int rd = r0 + sl;
+    const int s0 = rd * KC;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = 64 * i + lane;
       const int row = c / CPR, col = c % CPR;
-      sa[row * PITCH + col] = ca[i];
-      sw[row * PITCH + col] = cw[i];
+      *(u32x4_t*)&sa[row * PITCH + col] = ca[sl][i];
+      *(u32x4_t*)&sw[row * PITCH + col] = cw[sl][i];
     }
     // LDS accesses of one wave complete in order: its reads below see its
     // writes above; this keeps the compiler from reordering them
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
+    if constexpr (D > 1)
+      load_round(slc, min(rd + D, nrounds - 1) * KC);
+    else if (rd + 1 < nrounds)
+      load_round(slc, (rd + 1) * KC);
 #pragma unroll
     for (int s = 0; s < KC; ++s) {
-      if (s0 + s < kw) {
+      if (D > 1 || s0 + s < kw) {   // D > 1: whole rounds (host-checked)
         uint4 a[T], w[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -957,7 +1044,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
     }
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
-  }
+  });
   // partials of waves 1..3 into their own regions, summed by wave 0 in order
   floatx4_t* red = (floatx4_t*)s_t[wk];
   if (wk > 0) {
@@ -1023,16 +1110,23 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
   // +1.6%, batch 64 -8.5%, batch 16 -4%), and the row sums of squares of a
   // quarter must fit a wave's region.
   if (!rms || (M > 64 && 16 * T * 4 * kw * 4 <= sk2_region_bytes(T))) {
+    // 32 x 32 tiles with a whole number of 3-round groups: three rounds in
+    // flight per wave (cfg5 decode 3421 -> 3310 us per step, measured); the
+    // 16 x 16 tiles measured ~1% slower with it (batch-64 proj: 3 rounds)
+    const int xd = T == 2 && kw % 4 == 0 && (kw / 4) % 3 == 0 ? 3 : 1;
 #define ANN_SK2_R(E, R)                                                                          \
   if (T == 1) {                                                                                  \
     if (kw <= 6)                                                                                 \
-      hipLaunchKernelGGL((k_gemm_sk2<E, R, 6, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,   \
-                         eps, ea);                                                               \
+      hipLaunchKernelGGL((k_gemm_sk2<E, R, 6, 1, 1>), grid, dim3(256), 0, st, A, lda, W, M, N,   \
+                         K, eps, ea);                                                            \
     else                                                                                         \
-      hipLaunchKernelGGL((k_gemm_sk2<E, R, 8, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,   \
-                         eps, ea);                                                               \
+      hipLaunchKernelGGL((k_gemm_sk2<E, R, 8, 1, 1>), grid, dim3(256), 0, st, A, lda, W, M, N,   \
+                         K, eps, ea);                                                            \
+  } else if (xd == 1) {                                                                          \
+    hipLaunchKernelGGL((k_gemm_sk2<E, R, 4, 2, 1>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
+                       eps, ea);                                                                 \
   } else {                                                                                       \
-    hipLaunchKernelGGL((k_gemm_sk2<E, R, 4, 2>), grid, dim3(256), 0, st, A, lda, W, M, N, K,     \
+    hipLaunchKernelGGL((k_gemm_sk2<E, R, 4, 2, 3>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
                        eps, ea);                                                                 \
   }
 #define ANN_SK2(E)       \
@@ -1131,12 +1225,23 @@ hipError_t gemm_decode64(int epi, const bf16_t* A, int lda, const bf16_t* W, int
                          const EpiArgs& ea, hipStream_t st) {
   if (K % GM_BK != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
   dim3 grid((N + 63) / 64, (M + 63) / 64);
-  if (epi == EPI_STORE)
-    hipLaunchKernelGGL((k_gemm<EPI_STORE, 64, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
-  else if (epi == EPI_RELU2)
-    hipLaunchKernelGGL((k_gemm<EPI_RELU2, 64, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);
-  else
+  // four K tiles in flight per thread (cfg5 qkv / fc: 3310 -> 3017 us per
+  // decode step, measured; eight: 3073)
+  const bool deep = (K / GM_BK) % 4 == 0;
+#define ANN_D64(E)                                                                               \
+  if (!deep)                                                                                     \
+    hipLaunchKernelGGL((k_gemm<E, 64, 64>), grid, dim3(256), 0, st, A, lda, W, M, N, K, ea);     \
+  else                                                                                           \
+    hipLaunchKernelGGL((k_gemm_deep<E, 64, 64, 4>), grid, dim3(256), 0, st, A, lda, W, M, N, K,  \
+                       ea);
+  if (epi == EPI_STORE) {
+    ANN_D64(EPI_STORE)
+  } else if (epi == EPI_RELU2) {
+    ANN_D64(EPI_RELU2)
+  } else {
     return hipErrorInvalidValue;
+  }
+#undef ANN_D64
   return hipGetLastError();
 }
 
@@ -1165,6 +1270,17 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
   else hipLaunchKernelGGL((k_gemm_2w<E, 128, 256>), grid, dim3(256), 0, st, A, lda, W, M, N,   \
                           K, ea);                                                              \
   break;
+  // the decode lm_head (z of one row per sequence, up to 511 rows): four K
+  // tiles in flight per thread
+  if (epi == EPI_LOGITS && shape <= 1 && (K / GM_BK) % 4 == 0) {
+    if (shape == 0)
+      hipLaunchKernelGGL((k_gemm_deep<EPI_LOGITS, 64, GM_BN, 4>), grid, dim3(256), 0, st, A, lda,
+                         W, M, N, K, ea);
+    else
+      hipLaunchKernelGGL((k_gemm_deep<EPI_LOGITS, 128, GM_BN, 4>), grid, dim3(256), 0, st, A,
+                         lda, W, M, N, K, ea);
+    return hipGetLastError();
+  }
   switch (epi) {
     case EPI_STORE: ANN_GM(EPI_STORE)
     case EPI_RELU2: ANN_GM(EPI_RELU2)

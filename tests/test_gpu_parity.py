@@ -325,6 +325,32 @@ def test_decode_wide_batch_skinny_tiles(B):
     assert worst < LOGIT_TOL, worst
 
 
+def test_decode_deep_load_rings():
+    """Decode at 72 rows of a d = 768 model with a vocabulary above 8 d: the
+    qkv / fc projections on 64 x 64 MFMA tiles with four K tiles in flight,
+    the proj projection (K = 3072) on the LDS-staged skinny GEMM with three
+    rounds in flight per wave, and the lm_head on 128-row tiles with four K
+    tiles in flight; logits against the oracle."""
+    cfg = GPTConfig(vocab_size=8192, num_layers=2, num_heads=6, model_dim=768, seq_len=16,
+                    window=8, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 47, dense=True))
+    B = 72
+    tok = np.random.default_rng(48).integers(0, cfg.vocab_size, (B, 12))
+    print(f"case d=768 B={B} V=8192", flush=True)
+    eng = _engine(cfg, p, B)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :9], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :9], cache)[:, -1]).abs().max().item()
+    for i in range(9, 12):
+        t = tok[:, i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
+    assert worst < LOGIT_TOL, worst
+
+
 def test_decode_weight_prefetch_bitwise(monkeypatch):
     """From 16 rows the decode attention launch carries extra work-groups that
     read the next projections' weights ahead (this layer's o / fc / proj and
