@@ -498,17 +498,17 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int RB = PD_SLOTS / UD;    // rows per wave per batch
   const int nrow = r1 - r0, nb = (nrow + PD_NW * RB - 1) / (PD_NW * RB);
   const int K8 = d >> 3;
+  // Loads are unconditional (rows past this work-group's range and chunks
+  // past the row read clamped addresses; hdot zeroes those chunks and drops
+  // those rows), so the compiler can wait on one batch while the next is in
+  // flight instead of on every load.
   auto hload = [&](int k, uint4* w) {
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr) {
-      const int r = k * PD_NW * RB + wv + PD_NW * rr;
-      const bool ok = r < nrow;
-      const uint4* row = (const uint4*)(P.head + (size_t)(r0 + (ok ? r : 0)) * d);
+      const int r = min(k * PD_NW * RB + wv + PD_NW * rr, nrow - 1);
+      const uint4* row = (const uint4*)(P.head + (size_t)(r0 + r) * d);
 #pragma unroll
-      for (int u = 0; u < UD; ++u) {
-        const int c = lane + 64 * u;
-        w[rr * UD + u] = (ok && c < K8) ? row[c] : make_uint4(0u, 0u, 0u, 0u);
-      }
+      for (int u = 0; u < UD; ++u) w[rr * UD + u] = row[min(lane + 64 * u, K8 - 1)];
     }
   };
   u64 best[BM];
@@ -525,12 +525,13 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         for (int b = 0; b < BM; ++b) acc[b] = 0.f;
 #pragma unroll
         for (int u = 0; u < UD; ++u) {
+          // a chunk past the row adds exactly 0 (zero weights, finite x)
           const int c = lane + 64 * u;
-          if (c < K8) {
+          const bool cv = c < K8;
+          const uint4 wz = cv ? w[rr * UD + u] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-            for (int b = 0; b < BM; ++b)
-              acc[b] = pd_dot8(w[rr * UD + u], ((const uint4*)gin)[b * K8 + c], acc[b]);
-          }
+          for (int b = 0; b < BM; ++b)
+            acc[b] = pd_dot8(wz, ((const uint4*)gin)[b * K8 + (cv ? c : K8 - 1)], acc[b]);
         }
 #pragma unroll
         for (int b = 0; b < BM; ++b) {
@@ -547,18 +548,19 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       }
     }
   };
+  // batches in pairs (an odd count gets one batch of dropped rows); every
+  // load unconditional, the last refill re-reads the last batch (unused)
   uint4 wa[PD_SLOTS], wb[PD_SLOTS];
+  const int nbe = (nb + 1) & ~1;
   if (nb > 0) hload(0, wa);
   ll_poll(P.xx, BM * d2, (uint32_t*)sxs, tl, P.err);
   __syncthreads();
   pd_rms<BM>(sxs, gin, d, P.eps, red);
-  for (int k = 0; k < nb; k += 2) {
-    if (k + 1 < nb) hload(k + 1, wb);
+  for (int k = 0; k < nbe; k += 2) {
+    hload(k + 1, wb);
     hdot(k, wa);
-    if (k + 1 < nb) {
-      if (k + 2 < nb) hload(k + 2, wa);
-      hdot(k + 1, wb);
-    }
+    hload(min(k + 2, nbe - 1), wa);
+    hdot(k + 1, wb);
   }
 
   if (P.greedy) {

@@ -1270,17 +1270,6 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
   else hipLaunchKernelGGL((k_gemm_2w<E, 128, 256>), grid, dim3(256), 0, st, A, lda, W, M, N,   \
                           K, ea);                                                              \
   break;
-  // the decode lm_head (z of one row per sequence, up to 511 rows): four K
-  // tiles in flight per thread
-  if (epi == EPI_LOGITS && shape <= 1 && (K / GM_BK) % 4 == 0) {
-    if (shape == 0)
-      hipLaunchKernelGGL((k_gemm_deep<EPI_LOGITS, 64, GM_BN, 4>), grid, dim3(256), 0, st, A, lda,
-                         W, M, N, K, ea);
-    else
-      hipLaunchKernelGGL((k_gemm_deep<EPI_LOGITS, 128, GM_BN, 4>), grid, dim3(256), 0, st, A,
-                         lda, W, M, N, K, ea);
-    return hipGetLastError();
-  }
   switch (epi) {
     case EPI_STORE: ANN_GM(EPI_STORE)
     case EPI_RELU2: ANN_GM(EPI_RELU2)

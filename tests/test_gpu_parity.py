@@ -326,11 +326,11 @@ def test_decode_wide_batch_skinny_tiles(B):
 
 
 def test_decode_deep_load_rings():
-    """Decode at 72 rows of a d = 768 model with a vocabulary above 8 d: the
-    qkv / fc projections on 64 x 64 MFMA tiles with four K tiles in flight,
-    the proj projection (K = 3072) on the LDS-staged skinny GEMM with three
-    rounds in flight per wave, and the lm_head on 128-row tiles with four K
-    tiles in flight; logits against the oracle."""
+    """Decode at 72 rows of a d = 768 model: the qkv / fc projections on
+    64 x 64 MFMA tiles with four K tiles in flight, the proj projection
+    (K = 3072) on the LDS-staged skinny GEMM with three rounds in flight per
+    wave, and (vocabulary above 8 d) the lm_head on the 128-row MFMA tiles;
+    logits against the oracle."""
     cfg = GPTConfig(vocab_size=8192, num_layers=2, num_heads=6, model_dim=768, seq_len=16,
                     window=8, long_layers=(1,))
     p = perturb_lambdas(init_params(cfg, 47, dense=True))
