@@ -1,7 +1,8 @@
 // Persistent decode step for batch 1: embed, every layer, lm_head and the
-// greedy argmax of one token in ONE launch of one 512-thread work-group per
-// CU, all resident at once (model.py:223-263 for T = 1, sample.py:44-49
-// greedy).
+// greedy argmax of one token in ONE launch of G 512-thread work-groups, at
+// most one per CU, all resident at once (model.py:223-263 for T = 1,
+// sample.py:44-49 greedy).  The host picks G (3/4 of the CUs where the rows
+// fit: fewer work-groups exchange faster, measured).
 //
 // Why: at batch 1 a decode step is ~57 dependent phases whose own work is a
 // few microseconds of weight streaming; as separate kernels every phase pays
@@ -28,7 +29,7 @@
 // Every wait is bounded: after PD_SPIN polls (or once any work-group has
 // flagged a timeout in *err) it gives up and the kernel runs to its end, so
 // all waves always exit; the host reports a set flag as an error.  The grid
-// must be co-resident: one work-group per CU, a CU holds one (see pd_launch).
+// must be co-resident: G <= the CU count, a CU holds one (see pd_launch).
 #include <math.h>
 #include "common.h"
 #include "launch.h"
@@ -100,8 +101,9 @@ __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, ui
 }
 
 // Rows per wave of the K = d projections held in registers (U = UD chunks
-// each); the K = 4d projection holds one row of 4 UD chunks.
-constexpr int pd_rows_per_wave(int ud) { return ud == 3 ? 3 : 2; }
+// each); the K = 4d projection holds one row of 4 UD chunks.  Three for
+// d > 512: the 155M step fits 128-192 work-groups (neutral at 256, measured).
+constexpr int pd_rows_per_wave(int ud) { return ud >= 2 ? 3 : 2; }
 
 // Rows of a projection owned by work-group g: pairs [b, e) of npairs.
 __device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr) {
@@ -633,8 +635,8 @@ size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
   return (size_t)7 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
 }
 
-// Launch of the G work-groups.  The grid is one work-group per CU and a CU
-// holds one (occupancy checked), so once the stream's earlier work has
+// Launch of the G work-groups.  G is at most the CU count and a CU holds one
+// (occupancy checked), so once the stream's earlier work has
 // drained every work-group is resident; a plain launch is measured ~19 us per
 // step cheaper than a cooperative one (which the runtime serialises), and the
 // bounded waits end the kernel with the error flag set should residency ever

@@ -190,7 +190,9 @@ struct ann_ctx {
   int sp_topk = 0;
   uint64_t sp_seed = 0, sp_step = 0;
   // persistent batch-1 decode step
-  int n_cu = -1;         // CUs of the device (queried on first use)
+  // work-groups of the persistent step (one per CU, on 3/4 of the CUs where
+  // the model's rows fit that grid, else on all; 0: not possible; set on first use)
+  int pd_g = -1;
   bool pd_env = true;    // ANN_PERSIST=0 disables
   bool pd_coop = false;  // ANN_PERSIST_COOP=1: cooperative launch
   bool pd_clear = true;  // exchange area must be cleared before the next use
@@ -483,7 +485,7 @@ int pd_splits(const ann_ctx* c, int B, bool lng) {
   const int keys = lng ? c->c.max_ctx : (c->c.window < c->c.max_ctx ? c->c.window : c->c.max_ctx);
   int s = (keys + 127) / 128;
   if (s > PD_MAX_SLONG) s = PD_MAX_SLONG;
-  if (c->n_cu > 0 && s > c->n_cu / (B * c->c.H)) s = c->n_cu / (B * c->c.H);
+  if (c->pd_g > 0 && s > c->pd_g / (B * c->c.H)) s = c->pd_g / (B * c->c.H);
   return s < 1 ? 1 : s;
 }
 
@@ -491,17 +493,35 @@ int pd_splits(const ann_ctx* c, int B, bool lng) {
 bool persist_ok(ann_ctx* c, int B) {
   if (!c->pd_env || B != PD_BATCH || (c->prof_kind >= 0 && c->prof_kind != ANN_PROF_STEP))
     return false;
-  if (c->n_cu < 0) {
+  const ann_config& g = c->c;
+  if (c->pd_g < 0) {
     int dev = 0, n = 0, coop = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
       n = 0;
-    c->n_cu = (coop && n <= PD_MAX_G) ? n : 0;
+    // Fewer work-groups than CUs exchange faster: 155M batch-1 step 216.6 us
+    // on 256 work-groups, 205.8 on 192, 208.0 on 160, 209.1 on 128 (measured).
+    // ANN_PERSIST_G=n sets the grid (at most the CU count).
+    int pick = 0;
+    if (coop && n > 0 && n <= PD_MAX_G) {
+      const char* ge = getenv("ANN_PERSIST_G");
+      const int want = ge && atoi(ge) > 0 ? (atoi(ge) < n ? atoi(ge) : n) : (n * 3 / 4) & ~7;
+      const int cands[2] = {want, n};
+      for (int cand : cands) {
+        if (cand < 1) continue;
+        c->pd_g = cand;   // pd_splits reads it
+        if (decode_persist_fits(PD_BATCH, g.d, g.H, c->Dh, g.V, g.L, cand,
+                                pd_splits(c, PD_BATCH, true))) {
+          pick = cand;
+          break;
+        }
+      }
+    }
+    c->pd_g = pick;
   }
-  const ann_config& g = c->c;
-  return c->n_cu > 0 && g.n_long <= 8 &&
-         decode_persist_fits(B, g.d, g.H, c->Dh, g.V, g.L, c->n_cu, pd_splits(c, B, true));
+  return c->pd_g > 0 && g.n_long <= 8 &&
+         decode_persist_fits(B, g.d, g.H, c->Dh, g.V, g.L, c->pd_g, pd_splits(c, B, true));
 }
 
 int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
@@ -553,7 +573,7 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.eps = g.rms_eps;
   {
     ProfScope ps(c, ANN_PROF_STEP, st);
-    HIPCHK(decode_persist(P, B, c->Dh, c->n_cu, c->pd_coop, st));
+    HIPCHK(decode_persist(P, B, c->Dh, c->pd_g, c->pd_coop, st));
   }
   if (!greedy)
     HIPCHK(sample(c->sp<bf16_t>(c->sl.zb), g.V, B, g.V_sample, c->sp<SampParams>(c->sl.sp),
