@@ -18,13 +18,13 @@
 namespace ann {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
 // register-ring element: a native vector (an array of HIP's uint4 struct that
 // stays live across loop iterations is kept in scratch memory, not registers)
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// f(integral_constant<int, I>) for I = I0 .. N-1: register-ring slots indexed
-// by compile-time constants (a loop index, even unrolled, leaves the ring in
-// scratch memory)
+// f(integral_constant<int, I>) for I = I .. N-1: the slots of a register ring
+// indexed by compile-time constants
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   if constexpr (I < N) {
@@ -32,7 +32,6 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for<I + 1, N>(f);
   }
 }
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 // Epilogue for one output element (row m, column n) of accumulator y.
 template <int EPI>
@@ -581,7 +580,9 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   // and no conditional load in the loop; the last DEPTH refills re-read the
   // last tile (unused)
   const int KT = K / GM_BK;
-  static_for<0, DEPTH>([&](auto slc) __attribute__((always_inline)) { load_tile(slc, decltype(slc)::value * GM_BK); });
+  static_for<0, DEPTH>([&](auto slc) __attribute__((always_inline)) {
+    load_tile(slc, decltype(slc)::value * GM_BK);
+  });
   for (int kt0 = 0; kt0 < KT; kt0 += DEPTH)
   static_for<0, DEPTH>([&](auto slc) __attribute__((always_inline)) {
     const int kt = kt0 + decltype(slc)::value;
@@ -994,7 +995,9 @@ __global__ __launch_bounds__(256) void k_gemm_sk2(const bf16_t* __restrict__ A, 
   // D > 1 needs the round count a multiple of D (host-checked): no break and
   // no conditional load in the loop; the last D refills re-read the last round
   const int nrounds = (kw + KC - 1) / KC;
-  static_for<0, D>([&](auto slc) __attribute__((always_inline)) { load_round(slc, decltype(slc)::value * KC); });
+  static_for<0, D>([&](auto slc) __attribute__((always_inline)) {
+    load_round(slc, decltype(slc)::value * KC);
+  });
   for (int r0 = 0; r0 < nrounds; r0 += D)
   static_for<0, D>([&](auto slc) __attribute__((always_inline)) {
     constexpr int sl = decltype(slc)::value;
