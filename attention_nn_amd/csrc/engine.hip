@@ -500,13 +500,21 @@ bool persist_ok(ann_ctx* c, int B) {
         hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
       n = 0;
-    // Fewer work-groups than CUs exchange faster: 155M batch-1 step 216.6 us
-    // on 256 work-groups, 205.8 on 192, 208.0 on 160, 209.1 on 128 (measured).
-    // ANN_PERSIST_G=n sets the grid (at most the CU count).
+    // Fewer work-groups than CUs exchange faster, and a count dividing d/2
+    // (every projection's row pairs) keeps the work-groups equal: 155M
+    // batch-1 step 216 us on 256 work-groups, 203.4 on 192, 207.9 on 184 and
+    // 200, 208.7 on 176, 209.5 on 208, 209.1 on 128 (measured).  Default: the
+    // largest divisor of d/2 up to 3/4 of the CUs; ANN_PERSIST_G=n sets it.
     int pick = 0;
     if (coop && n > 0 && n <= PD_MAX_G) {
       const char* ge = getenv("ANN_PERSIST_G");
-      const int want = ge && atoi(ge) > 0 ? (atoi(ge) < n ? atoi(ge) : n) : (n * 3 / 4) & ~7;
+      int want = 0;
+      if (ge && atoi(ge) > 0) {
+        want = atoi(ge) < n ? atoi(ge) : n;
+      } else {
+        for (int q = n * 3 / 4; q >= 1 && !want; --q)
+          if ((g.d / 2) % q == 0) want = q;
+      }
       const int cands[2] = {want, n};
       for (int cand : cands) {
         if (cand < 1) continue;
