@@ -34,7 +34,14 @@ Parity status per function (what pins each one; checked in tests/):
                           window == full while pos < window
   softcap               : closed form, bounds (0, 23), monotonicity
   logits (whole)        : closed-form known answer of the degenerate init
-                          (Wo = proj = x0 = 0 => x_L is a scaled x0),
+                          (Wo = proj = x0 = 0 => x_L is a scaled x0);
+                          the dense wiring (mix_attn, mix_mlp, mlp_branch,
+                          the q/k/v slices, mask, every lambda slot) by
+                          closed forms in numpy -- Wq = Wk = 0 with fc = 0
+                          (uniform attention over the kept keys, zero MLP)
+                          and Wv = 0 (zero attention, dense MLP) -- with
+                          distinct lambdas, where each planted index or
+                          wiring mistake fails (tests/test_oracle_wiring.py);
                           KV-cache decode == full recompute, fp64 forward
   softcap_ce            : torch.nn.functional.cross_entropy on the softcapped
                           logits; uniform z => loss = log V exactly
@@ -134,7 +141,25 @@ def attention(q, k, v, keep, scale, mlx_fallback_attn=False, banded_bf16=False):
     underflows in fp32), softmax(precise=True) runs in fp32 and returns bf16,
     and P.V is a bf16 matmul.  The 512-query bands (model.py:155-169) never
     drop an allowed key (ks = max(0, qs - W) <= i - W + 1), so the band
-    structure itself changes nothing and is not restated."""
+    structure itself changes nothing and is not restated.
+
+    Long inputs are processed in blocks of query rows, each against the key
+    columns its rows keep (softmax is per row and a dropped key contributes an
+    exact zero), which bounds the memory of the score matrix."""
+    Tq, Tk = keep.shape
+    if Tq * Tk <= (1 << 22):
+        return _attention_block(q, k, v, keep, scale, mlx_fallback_attn, banded_bf16)
+    outs = []
+    for qs in range(0, Tq, 512):
+        qe = min(qs + 512, Tq)
+        cols = torch.nonzero(keep[qs:qe].any(0)).flatten()
+        ks, ke = (int(cols[0]), int(cols[-1]) + 1) if cols.numel() else (0, 1)
+        outs.append(_attention_block(q[:, :, qs:qe], k[:, :, ks:ke], v[:, :, ks:ke],
+                                     keep[qs:qe, ks:ke], scale, mlx_fallback_attn, banded_bf16))
+    return torch.cat(outs, dim=2)
+
+
+def _attention_block(q, k, v, keep, scale, mlx_fallback_attn, banded_bf16):
     if banded_bf16:
         s = bf(bf(q @ k.transpose(-1, -2)) * scale)
         s = s.masked_fill(~keep, float("-inf"))
@@ -149,6 +174,22 @@ def attention(q, k, v, keep, scale, mlx_fallback_attn=False, banded_bf16=False):
     s = s.masked_fill(~keep, float("-inf"))
     p = torch.softmax(s, dim=-1)
     return bf(p @ v)
+
+
+# -- model.py:255-260: the two residual mixes and the MLP branch ----------------
+def mix_attn(x, y, x0, r0, p0, xl):
+    """model.py:256, eager bf16 left to right: (r0*x + p0*y) + xl*x0."""
+    return bf(bf(bf(r0 * x) + bf(p0 * y)) + bf(xl * x0))
+
+
+def mix_mlp(x, y, x0, r1, p1, xl):
+    """model.py:260: r1*x + p1*y (the embedding stream x0 does not enter)."""
+    return bf(bf(r1 * x) + bf(p1 * y))
+
+
+def mlp_branch(h, fc, proj):
+    """model.py:258-259: bf16(relu2(bf16(h @ fc)) @ proj)."""
+    return bf(relu2(bf(h @ fc)) @ proj)
 
 
 class Prepared:
@@ -187,11 +228,13 @@ class KVCache:
 
 
 def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=False,
-            banded_bf16=False):
+            banded_bf16=False, last_only=False):
     """Forward of ``tokens`` (B,T) placed at positions [start, start+T) where
     start = cache.length (0 without a cache).  Returns softcapped fp32 logits
     (B,T,V).  With ``cache`` the new K/V are appended (KV-cache decode);
-    without it this is exactly ``GPT.logits`` (model.py:223-263)."""
+    without it this is exactly ``GPT.logits`` (model.py:223-263).
+    ``last_only`` computes the lm_head for the last row only (B,1,V): the
+    rows of the lm_head product are independent, so that row is unchanged.""" 
     cfg = prep.cfg
     tokens = torch.as_tensor(tokens, dtype=torch.long)
     B, T = tokens.shape
@@ -221,12 +264,12 @@ def forward(prep, tokens, cache=None, mlx_fallback_attn=False, return_hidden=Fal
         y = attention(q, k, v, keep, cfg.attn_scale, mlx_fallback_attn,  # :251-254
                       banded_bf16)
         y = bf(y.transpose(1, 2).reshape(B, T, d) @ prep.wo[l])        # :255
-        r0, p0, xl = prep.resid[l, 0], prep.post[l, 0], prep.x0l[l]
-        x = bf(bf(bf(r0 * x) + bf(p0 * y)) + bf(xl * x0))            # :256
+        x = mix_attn(x, y, x0, prep.resid[l, 0], prep.post[l, 0], prep.x0l[l])   # :256
         h = rms(x)                                                  # :257
-        y = bf(relu2(bf(h @ prep.fc[l])) @ prep.proj[l])            # :258-259
-        r1, p1 = prep.resid[l, 1], prep.post[l, 1]
-        x = bf(bf(r1 * x) + bf(p1 * y))                             # :260
+        y = mlp_branch(h, prep.fc[l], prep.proj[l])                 # :258-259
+        x = mix_mlp(x, y, x0, prep.resid[l, 1], prep.post[l, 1], prep.x0l[l])    # :260
+    if last_only:
+        x = x[:, -1:]
     hfin = rms(x)
     z = bf(hfin @ prep.lm_head)                                     # :262
     out = softcap(z)                                                # :263
