@@ -1,6 +1,7 @@
 """Build libattnnn.so (the gfx950 kernels + C ABI) in-tree with hipcc.
 
-    python -m attention_nn_amd.build      # or attention_nn_amd.build.build()
+    python -m attention_nn_amd.build              # or attention_nn_amd.build.build()
+    python -m attention_nn_amd.build --changed    # only sources newer than their objects
 
 Every ``csrc/*.hip`` file is compiled for gfx950 only, then linked into
 ``attention_nn_amd/libattnnn.so``.  Objects go to ``attention_nn_amd/_build``.
@@ -37,14 +38,29 @@ def _compile(src):
     return obj
 
 
-def build(verbose=False):
+def _stale(src, headers):
+    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(f) > t for f in [src, *headers])
+
+
+def build(verbose=False, changed_only=False):
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
-    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    headers.append(os.path.join(ROOT, "include", "attnnn.h"))
+    todo = [s for s in srcs if _stale(s, headers)] if changed_only else srcs
+    jobs = min(max(len(todo), 1), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        list(ex.map(_compile, todo))
+    if verbose and changed_only:
+        print("compiled: " + (", ".join(os.path.basename(s) for s in todo) or "nothing"))
+    objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in srcs]
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    # -z defs: an unresolved symbol fails the link instead of the first load
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-z,defs", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stderr}")
@@ -55,5 +71,5 @@ def build(verbose=False):
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, changed_only="--changed" in sys.argv[1:])
     sys.exit(0)

@@ -106,3 +106,40 @@ __device__ __forceinline__ bf16_t relu2_bf(float y) {
 __device__ __forceinline__ uint32_t zkey(bf16_t h) {
   return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
 }
+
+// ---- tagged words ("LL" exchange) -------------------------------------------
+// A 64-bit word carries 32 bits of data and a 32-bit tag, written with one
+// relaxed device-scope store and read with device-scope loads: a reader that
+// sees the tag it waits for has that writer's data of the same word.  Only
+// single-location coherence is relied on -- no fence, no ordering between
+// different words.
+typedef unsigned long long u64;
+constexpr unsigned LL_SPIN = 1u << 18;   // polls before a wait gives up
+
+__device__ __forceinline__ void ll_store(u64* p, uint32_t v, uint32_t tag) {
+  __hip_atomic_store(p, ((u64)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ll_load(const u64* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until the word carries `tag` and return its data.  Bounded: after
+// LL_SPIN polls, or at once when another wait has already given up (*err set),
+// it sets *err and returns whatever it read.  Two polls stay in flight, so a
+// ready word is seen about one load latency after it lands instead of up to
+// two; no sleep between them (measured faster).
+__device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
+  u64 a = ll_load(p);
+  for (unsigned s = 0;; s += 2) {
+    const u64 b = ll_load(p);
+    if ((uint32_t)(a >> 32) == tag) return (uint32_t)a;
+    if ((s & 127u) == 0 && s) {
+      if (s >= LL_SPIN) {
+        atomicOr(err, 1u);
+        return (uint32_t)b;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return (uint32_t)b;
+    }
+    a = ll_load(p);
+    if ((uint32_t)(b >> 32) == tag) return (uint32_t)b;
+  }
+}

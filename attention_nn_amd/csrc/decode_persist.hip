@@ -26,7 +26,7 @@
 // work-group -> xk, work-group 0 picks the token and advances pos; otherwise
 // z is stored for the sampler kernel.
 //
-// Every wait is bounded: after PD_SPIN polls (or once any work-group has
+// Every wait is bounded: after LL_SPIN polls (or once any work-group has
 // flagged a timeout in *err) it gives up and the kernel runs to its end, so
 // all waves always exit; the host reports a set flag as an error.  The grid
 // must be co-resident: G <= the CU count, a CU holds one (see pd_launch).
@@ -42,7 +42,6 @@ constexpr int PD_SLOTS = 12;                 // 16-byte weight chunks per lane i
 constexpr int PD_RMAX = PD_NW * PD_SLOTS;    // projection rows per work-group (U = 1)
 constexpr int PD_KW = 16;                    // keys per wave chunk
 constexpr uint32_t PD_PH = 256;              // tags per step
-constexpr unsigned PD_SPIN = 1u << 18;
 
 typedef __bf16 pd_bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -57,31 +56,6 @@ __device__ __forceinline__ float pd_dot8(const uint4& w, const uint4& x, float c
   return pd_dot2(w.w, x.w, c);
 }
 
-__device__ __forceinline__ void ll_store(u64* p, uint32_t v, uint32_t tag) {
-  __hip_atomic_store(p, ((u64)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ u64 ll_load(const u64* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Wait until the word carries `tag`; bounded (see the file comment).  Two
-// polls stay in flight, so a ready word is seen about one load latency after
-// it lands instead of up to two; no sleep between them (measured faster).
-__device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
-  u64 a = ll_load(p);
-  for (unsigned s = 0;; s += 2) {
-    const u64 b = ll_load(p);
-    if ((uint32_t)(a >> 32) == tag) return (uint32_t)a;
-    if ((s & 127u) == 0 && s) {
-      if (s >= PD_SPIN) {
-        atomicOr(err, 1u);
-        return (uint32_t)b;
-      }
-      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return (uint32_t)b;
-    }
-    a = ll_load(p);
-    if ((uint32_t)(b >> 32) == tag) return (uint32_t)b;
-  }
-}
 // dst[i] = data of src[i] for i < n, all loads of a thread issued first.
 __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, uint32_t tag,
                                         unsigned* err) {

@@ -116,7 +116,7 @@ SLayout ws_layout(const ann_config& c) {
   s.ao = off; off += up(M * d * 2);
   s.hn = off; off += up(M * d * 2);
   s.hid = off; off += up(M * 4 * d * 2);
-  s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 2) * 4);
+  s.part = off; off += up(B * c.H * MAX_SPLIT * (Dh + 1) * 8);
   s.zb = off; off += up(B * (size_t)c.V * 2);
   s.pd = off; off += (s.pd_bytes = up(pd_layout(c, 0)));
   // training-forward loss: per-(128-column tile, row) partial sums, target
@@ -188,6 +188,7 @@ struct ann_ctx {
   bool sp_valid = false;
   float sp_temp = 0.f;
   int sp_topk = 0;
+  int sp_rows = 0;  // rows whose draw counters the last write set
   uint64_t sp_seed = 0, sp_step = 0;
   // persistent batch-1 decode step
   // work-groups of the persistent step (one per CU, on 3/4 of the CUs where
@@ -195,7 +196,9 @@ struct ann_ctx {
   int pd_g = -1;
   bool pd_env = true;    // ANN_PERSIST=0 disables
   bool pd_coop = false;  // ANN_PERSIST_COOP=1: cooperative launch
-  bool pd_clear = true;  // exchange area must be cleared before the next use
+  // the persistent step's exchange area, the error word and the decode
+  // attention's ticket counters must be cleared before the next decode step
+  bool dec_clear = true;
   // decode (batch >= 16): prefetch work-groups per attention launch that read
   // the next projections' weights ahead; -1 = not read yet, -2 = sized by
   // bytes, >= 0 = fixed by ANN_PREFETCH_WG
@@ -319,7 +322,8 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
   bf16_t* q = c->sp<bf16_t>(c->sl.q);
   bf16_t* ao = c->sp<bf16_t>(c->sl.ao);
   bf16_t* hid = c->sp<bf16_t>(c->sl.hid);
-  float* part = c->sp<float>(c->sl.part);
+  u64* part = c->sp<u64>(c->sl.part);
+  unsigned* err = (unsigned*)(c->ws + c->sl.pd + pd_layout(g, 8));
   const int32_t* pos = c->sp<int32_t>(c->sl.pos);
   const float* lam = (const float*)(c->w + c->wl.lam);
   const float* cs = (const float*)(c->w + c->wl.cs);
@@ -378,7 +382,7 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
       {
         ProfScope ps(c, ANN_PROF_ATTN, st);
         HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part,
-                           c->sp<unsigned>(c->sl.acnt), ao, B, H, Dh, g.max_ctx, g.window, lng,
+                           c->sp<unsigned>(c->sl.acnt), err, ao, B, H, Dh, g.max_ctx, g.window, lng,
                            g.attn_scale, g.rms_eps, ns, pf, st));
       }
       rc = proj(c, ANN_PROF_O, EPI_RESID_ATTN, PRE_PLAIN, c->layer_w(l, c->wl.o), ao, d, M, d, d,
@@ -455,12 +459,16 @@ int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, flo
   return ANN_OK;
 }
 
-// Bring the device sampling parameters / draw counters in line with s.
+// Bring the device sampling parameters / draw counters in line with s.  The
+// sampler kernel reads the temperature from the device (0 = greedy, which it
+// also serves above 8 rows), so a greedy call after a sampled one must write
+// it; greedy draws nothing, so its seed / step / counters need not match.
+// The counters cover the rows of the last write: a call with more rows writes.
 int sync_sampling(ann_ctx* c, const ann_sampling* s, int B, hipStream_t st) {
   const bool greedy = s->temperature == 0.f;
-  if (greedy) return ANN_OK;  // the greedy path reads no parameters
-  if (c->sp_valid && c->sp_temp == s->temperature && c->sp_topk == s->top_k &&
-      c->sp_seed == s->seed && c->sp_step == s->step)
+  if (c->sp_valid && c->sp_temp == s->temperature &&
+      (greedy || (c->sp_topk == s->top_k && c->sp_seed == s->seed && c->sp_step == s->step &&
+                  B <= c->sp_rows)))
     return ANN_OK;
   HIPCHK(set_sampling(c->sp<SampParams>(c->sl.sp), c->sp<unsigned long long>(c->sl.steps), B,
                       s->temperature, s->top_k, s->seed, s->step, st));
@@ -469,6 +477,7 @@ int sync_sampling(ann_ctx* c, const ann_sampling* s, int B, hipStream_t st) {
   c->sp_topk = s->top_k;
   c->sp_seed = s->seed;
   c->sp_step = s->step;
+  c->sp_rows = B;
   return ANN_OK;
 }
 
@@ -693,13 +702,13 @@ int ann_check_device(ann_ctx* c, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
-  if (c->pd_clear) return ANN_OK;   // the persistent step has not run since binding
+  if (c->dec_clear) return ANN_OK;   // no decode step has run since binding
   unsigned* err = (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8));
   unsigned h = 0;
   HIPCHK(hipMemcpy(&h, err, sizeof h, hipMemcpyDeviceToHost));
   if (h) {
     HIPCHK(hipMemset(err, 0, sizeof h));
-    return fail(ANN_E_HIP, "persistent decode: a cross-work-group wait timed out");
+    return fail(ANN_E_HIP, "decode step: a bounded cross-work-group wait timed out");
   }
   return ANN_OK;
 }
@@ -767,7 +776,7 @@ int ann_bind(ann_ctx* c, void* wbuf, size_t wbytes, void* kv, size_t kvbytes, vo
   c->w = (uint8_t*)wbuf;
   c->kv = (uint8_t*)kv;
   c->ws = (uint8_t*)workspace;
-  c->pd_clear = true;
+  c->dec_clear = true;
   c->bound = true;
   c->len = 0;
   c->B = 0;
@@ -884,9 +893,10 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   rc = sync_sampling(c, s, B, st);
   if (rc) return rc;
   const bool greedy = s->temperature == 0.f;
-  if (c->pd_clear && persist_ok(c, B)) {   // tags start from a clean area
+  if (c->dec_clear) {   // tags, tickets and the error word start from zero
     HIPCHK(hipMemsetAsync(c->ws + c->sl.pd, 0, c->sl.pd_bytes, st));
-    c->pd_clear = false;
+    HIPCHK(hipMemsetAsync(c->ws + c->sl.acnt, 0, (size_t)c->c.max_batch * c->c.H * 4, st));
+    c->dec_clear = false;
   }
   if (c->use_graph && c->prof_kind < 0)
     rc = decode_graph(c, tokens, B, greedy, out_tok, logits, st);

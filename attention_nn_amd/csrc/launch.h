@@ -147,10 +147,12 @@ struct WeightPrefetch {
 };
 
 // Decode attention with fused QK-norm / RoPE / KV append (one token per
-// sequence) -> out (B, H*Dh) bf16.  part: split scratch (B, H, nsplit, Dh + 1);
-// cnt: B*H arrival counters, zero between calls.
+// sequence) -> out (B, H*Dh) bf16.  part: split scratch of tagged words
+// (B, H, nsplit, Dh + 1); cnt: B*H ticket counters, multiples of 64 between
+// calls (zero before the first); err: set if a bounded wait gave up.
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
-                       const float* cs, const float* sn, float* part, unsigned* cnt, bf16_t* out,
+                       const float* cs, const float* sn, u64* part, unsigned* cnt, unsigned* err,
+                       bf16_t* out,
                        int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
                        float eps, int nsplit, const WeightPrefetch& pf, hipStream_t st);
 

@@ -1,26 +1,40 @@
-"""Token shards of the training data (``train.py:27-62``).
+"""Token shards of the training data: the ``.bin`` format and batch order of
+``train.py:27-62``.
 
-A shard is a ``.bin`` file: a header of 256 int32 (header[0] = 20240520,
-header[2] = token count) followed by the tokens as uint16.  ``load_shard``
-memory-maps the tokens; ``batch_iterator`` yields consecutive (inputs,
-targets) int32 batches of shape (B, T), targets being the inputs shifted by
-one token, cycling through the shards in order, with ``start_tokens``
-fast-forwarding a resumed run without reading data.
+A shard is a header of 256 little-endian int32 (word 0 = 20240520, word 2 =
+token count) followed by the tokens as little-endian uint16.
+
+Batch order.  With span = B*T, a batch is the span + 1 consecutive tokens
+starting at some offset p of a shard (inputs = the first span, targets = the
+last span).  A shard of n tokens has *room* n - span - 1: the offsets that
+still fit are exactly the p < room, and the shard is walked at p = p0,
+p0 + span, ... below its room, after which the next shard (cyclically) starts
+at p = 0.  A resumed run skips ``start_tokens`` counted over the rooms of
+the shards in order (modulo their sum), which is how the reference's resume
+counts them: the skip lands in the shard whose cumulative room first
+exceeds it, at the remainder.  That equals skipping start_tokens / span
+batches while the skip stays inside the first shard, or when every room is a
+multiple of span; past a shard whose room is not, the resumed offset is the
+reference's, not the batch boundary a continuous run would reach.
 """
+
+import itertools
 
 import numpy as np
 
 SHARD_MAGIC = 20240520
 HEADER_INTS = 256
+HEADER_BYTES = HEADER_INTS * 4
 
 
 def load_shard(path):
     """Tokens of one shard as a read-only uint16 memmap (``train.py:27-33``)."""
-    header = np.fromfile(path, dtype=np.int32, count=HEADER_INTS)
-    if header.size < HEADER_INTS or int(header[0]) != SHARD_MAGIC:
+    with open(path, "rb") as f:
+        head = np.frombuffer(f.read(HEADER_BYTES), dtype="<i4")
+    if head.size != HEADER_INTS or int(head[0]) != SHARD_MAGIC:
         raise ValueError(f"{path}: magic number mismatch")
-    n = int(header[2])
-    return np.memmap(path, dtype=np.uint16, mode="r", offset=HEADER_INTS * 4, shape=(n,))
+    count = int(head[2])
+    return np.memmap(path, dtype="<u2", mode="r", offset=HEADER_BYTES, shape=(count,))
 
 
 def write_shard(path, tokens, version=1):
@@ -28,44 +42,32 @@ def write_shard(path, tokens, version=1):
     tokens = np.asarray(tokens)
     if tokens.size and (tokens.min() < 0 or tokens.max() > 65535):
         raise ValueError("shard tokens must fit in uint16")
-    header = np.zeros(HEADER_INTS, dtype=np.int32)
-    header[0], header[1], header[2] = SHARD_MAGIC, version, tokens.size
+    head = np.zeros(HEADER_INTS, dtype="<i4")
+    head[[0, 1, 2]] = SHARD_MAGIC, version, tokens.size
     with open(path, "wb") as f:
-        f.write(header.tobytes())
-        f.write(tokens.astype(np.uint16).tobytes())
+        f.write(head.tobytes() + tokens.astype("<u2").tobytes())
+
+
+def resume_point(rooms, start_tokens):
+    """(shard index, offset) where a run resumed after ``start_tokens`` begins."""
+    ends = np.cumsum(rooms)
+    skip = int(start_tokens) % int(ends[-1])
+    shard = int(np.searchsorted(ends, skip, side="right"))
+    return shard, skip - (int(ends[shard - 1]) if shard else 0)
 
 
 def batch_iterator(shards, batch_size, seq_len, start_tokens=0):
-    """Endless (inputs, targets) int32 numpy batches of shape (B, T)
-    (``train.py:36-62``).
-
-    Each batch reads B*T + 1 consecutive tokens at the current offset; the
-    offset advances by B*T.  A shard whose remaining tokens cannot hold the
-    next span is left for the next shard (cyclic), from its start.
-    ``start_tokens`` skips that many tokens first, counted as the reference
-    counts them: over shard lengths minus (B*T + 1).  That equals skipping
-    start_tokens / (B*T) batches while the skip stays inside the first shard
-    (or when every such length is a multiple of B*T); past a shard whose
-    length is not, the resumed offset is the reference's, not the batch
-    boundary a continuous run would reach."""
+    """Endless (inputs, targets) int32 numpy batches of shape (B, T) in the
+    order described in the module docstring (``train.py:36-62``)."""
     if not isinstance(shards, (list, tuple)):
         shards = [shards]
     span = batch_size * seq_len
-    sizes = [len(s) - span - 1 for s in shards]
-    if any(n <= 0 for n in sizes):
+    rooms = [len(s) - span - 1 for s in shards]
+    if min(rooms) <= 0:
         raise ValueError("every shard must hold more than batch_size * seq_len + 1 tokens")
-    offset = start_tokens % sum(sizes)
-    si = 0
-    while offset >= sizes[si]:
-        offset -= sizes[si]
-        si += 1
-    pos = offset
-    while True:
-        tokens = shards[si]
-        if pos + span + 1 >= len(tokens):
-            si = (si + 1) % len(shards)
-            pos = 0
-            tokens = shards[si]
-        buf = np.asarray(tokens[pos:pos + span + 1]).astype(np.int32)
-        yield buf[:-1].reshape(batch_size, seq_len), buf[1:].reshape(batch_size, seq_len)
-        pos += span
+    first, p0 = resume_point(rooms, start_tokens)
+    order = itertools.chain(range(first, len(shards)), itertools.cycle(range(len(shards))))
+    for n, si in enumerate(order):
+        for p in range(p0 if n == 0 else 0, rooms[si], span):
+            window = np.asarray(shards[si][p:p + span + 1], dtype=np.int32)
+            yield window[:span].reshape(batch_size, seq_len), window[1:].reshape(batch_size, seq_len)

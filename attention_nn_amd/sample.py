@@ -44,6 +44,14 @@ def sample(prompt, steps, temperature=0.8, top_k=50, seed=None, *, params=None, 
     prompt: str (tiktoken GPT-2), a list of ids, or a (B, T) array of ids.
     Returns the generated ids: a list for a single prompt, (B, steps) array
     for a batch.  ``engine`` may be passed to reuse packed weights / buffers.
+
+    The sampled ids stay on the device: each step feeds the next one there,
+    and a device record of every step is copied to the host once at the end.
+    ``on_token`` (called with each step's (B,) ids, in order) receives them
+    through a pinned host buffer and one event per step, as they complete,
+    without stopping the device queue.  The host waits on the device only
+    when the context slides past seq_len (the re-prefill needs the ids) and
+    at the end, where the persistent step's bounded waits are also checked.
     """
     ids = np.asarray(_encode(prompt) if not hasattr(prompt, "shape") else prompt)
     single = ids.ndim == 1
@@ -53,6 +61,8 @@ def sample(prompt, steps, temperature=0.8, top_k=50, seed=None, *, params=None, 
     B, T0 = ids.shape
     if T0 < 1:
         raise ValueError("empty prompt")
+    if steps < 0:
+        raise ValueError("steps must be >= 0")
     if engine is None:
         if params is None or cfg is None:
             raise ValueError("pass params and cfg, or an engine")
@@ -61,21 +71,42 @@ def sample(prompt, steps, temperature=0.8, top_k=50, seed=None, *, params=None, 
     cfg = engine.cfg
     seq_len = min(cfg.seq_len, engine.max_ctx)
     seed = int(np.random.SeedSequence().entropy % (2**63)) if seed is None else int(seed)
+    if steps == 0:
+        return [] if single else np.empty((B, 0), np.int64)
 
-    hist = ids.copy()
-    out = np.empty((B, steps), dtype=np.int64)
+    dev = engine.device
+    rec = torch.empty((steps, B), dtype=torch.int32, device=dev)     # every step's ids
+    host = torch.empty((steps, B), dtype=torch.int32, pin_memory=True)
+    pending = []            # (step, event) of host copies not yet handed to on_token
+
+    def emit(block):
+        while pending and (block or pending[0][1].query()):
+            i, ev = pending.pop(0)
+            ev.synchronize()
+            on_token(host[i].numpy().astype(np.int64))
+
+    hist = ids.copy()       # host ids up to the last slide
+    n_hist = 0              # generated ids already appended to hist
     cur = None
     for i in range(steps):
         if i == 0 or engine.length + 1 > seq_len:
-            ctx = hist[:, -seq_len:]
-            cur, _ = engine.prefill(ctx, temperature, top_k, seed, i)
+            if i > 0:       # the window slides (sample.py:43): bring the new ids to the host
+                hist = np.concatenate([hist, rec[n_hist:i].cpu().numpy().T.astype(np.int64)], 1)
+                n_hist = i
+            cur, _ = engine.prefill(hist[:, -seq_len:], temperature, top_k, seed, i)
         else:
             cur, _ = engine.decode(cur, temperature, top_k, seed, i, out=cur)
-        nxt = cur.cpu().numpy().astype(np.int64)
-        out[:, i] = nxt
-        hist = np.concatenate([hist, nxt[:, None]], axis=1)
+        rec[i].copy_(cur)
         if on_token is not None:
-            on_token(nxt)
+            host[i].copy_(rec[i], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            pending.append((i, ev))
+            emit(False)
+    out = rec.cpu().numpy().T.astype(np.int64)
+    if on_token is not None:
+        emit(True)
+    engine.check_device()
     return list(out[0]) if single else out
 
 

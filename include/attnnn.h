@@ -221,10 +221,11 @@ size_t ann_op_normuon_ws_bytes(int32_t batch, int32_t M, int32_t N);
 int ann_op_normuon(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
                    float beta2, float* out, void* ws, size_t ws_bytes, void* stream);
 
-/* Device status of the persistent batch-1 decode step (no reference
- * counterpart).  Its cross-work-group waits are bounded; one that gives up
- * sets a device flag and the step's output is not valid.  Synchronises
- * `stream`, returns ANN_E_HIP (and clears the flag) if it is set, else ANN_OK. */
+/* Device status of the decode steps (no reference counterpart).  The
+ * cross-work-group waits of the persistent batch-1 step and of the decode
+ * attention's split combine are bounded; one that gives up sets a device flag
+ * and the step's output is not valid.  Synchronises `stream`, returns
+ * ANN_E_HIP (and clears the flag) if it is set, else ANN_OK. */
 int ann_check_device(ann_ctx* ctx, void* stream);
 
 #ifdef __cplusplus

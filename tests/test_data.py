@@ -80,3 +80,41 @@ def test_start_tokens_offset_past_an_unaligned_shard(tmp_path):
     assert int(x[0, 0]) == 500 + 13
     cont = list(itertools.islice(batch_iterator(sh, 2, 16), 16))
     assert int(cont[15][0][0, 0]) == 500
+
+
+def _stream_by_walking(shards, B, T, start, n):
+    """The batch starts of the order as specified: skip `start` tokens over the
+    shard rooms, then walk each shard by spans below its room, cyclically."""
+    span = B * T
+    rooms = [len(s) - span - 1 for s in shards]
+    skip = start % sum(rooms)
+    si = 0
+    while skip >= rooms[si]:
+        skip -= rooms[si]
+        si += 1
+    out, p = [], skip
+    while len(out) < n:
+        if p >= rooms[si]:
+            si, p = (si + 1) % len(shards), 0
+            continue
+        out.append((si, p))
+        p += span
+    return out
+
+
+@pytest.mark.parametrize("sizes,B,T", [([500, 300, 420], 2, 16), ([97, 61], 1, 7),
+                                       ([40, 30], 1, 10), ([1000], 4, 8)])
+def test_order_equals_specification(tmp_path, sizes, B, T):
+    """Against a step-by-step walk of the order at many resume offsets,
+    including every offset inside the first few spans and past each shard."""
+    sh = _shards(tmp_path, sizes)
+    base = np.concatenate([[0], np.cumsum(sizes)])
+    rooms = [n - B * T - 1 for n in sizes]
+    starts = set(range(0, 3 * B * T)) | {sum(rooms[:i]) + d for i in range(len(sizes) + 1)
+                                         for d in (-1, 0, 1)} | {sum(rooms) * 2 + 5}
+    for st in sorted(s for s in starts if s >= 0):
+        want = _stream_by_walking(sh, B, T, st, 2 * len(sizes) + 6)
+        got = list(itertools.islice(batch_iterator(sh, B, T, start_tokens=st), len(want)))
+        for (si, p), (x, y) in zip(want, got):
+            assert int(x[0, 0]) == int(base[si] + p) % 65536, (st, si, p)
+            assert int(y[-1, -1]) == int(base[si] + p + B * T) % 65536

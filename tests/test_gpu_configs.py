@@ -1,0 +1,242 @@
+"""GPU parity at the model shapes of the benchmark's larger configurations
+(reference ``sample.py:42-51`` running ``model.py:223-263``), through the C ABI.
+
+Each test runs the whole batch on the GPU -- so the kernels and tile shapes
+those workloads use are the ones exercised -- and checks a few rows against
+the oracle's KV-cache forward (batch rows are independent; the oracle
+computes the lm_head of the last row only).  Sampled tokens are checked for
+every row against the oracle sampler applied to the engine's own logits of
+that step (the draws use Philox with counter (step, row)).
+
+Tolerances: the north star's 2e-2 max-abs on softcapped logits; draws equal.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.ref_model as R
+import oracle.ref_sample as S
+from attention_nn_amd.config import GPTConfig, cfg_small_h4
+from attention_nn_amd.weights import init_params, perturb_lambdas
+from tests.test_gpu_parity import LOGIT_TOL, _greedy_gpu, _sample_small
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import attention_nn_amd._lib as L
+    L.lib()
+
+
+def _engine(cfg, params, B, ctx, tokens):
+    from attention_nn_amd.engine import Engine
+    return Engine(cfg, params, max_batch=B, max_ctx=ctx, max_tokens=tokens)
+
+
+def _run_case(cfg, params, B, T0, steps, rows, temp, k, seed, ctx):
+    """Prefill B prompts of T0 tokens, then `steps` teacher-forced decode
+    steps, all with (temp, k) sampling and logits; returns the worst logit
+    gap over the checked rows and the number of draws checked."""
+    rng = np.random.default_rng(B * 7 + T0)
+    tok = rng.integers(0, min(50257, cfg.vocab_size), (B, T0 + steps))
+    eng = _engine(cfg, params, B, ctx, B * T0)
+    prep = R.Prepared(cfg, params)
+    cache = R.KVCache(cfg.num_layers)
+    print(f"  prefill B={B} T={T0}", flush=True)
+    nxt, lg = eng.prefill(tok[:, :T0], temp, k, seed=seed, step=0, want_logits=True)
+    ref = R.forward(prep, tok[rows, :T0], cache, last_only=True)[:, -1]
+    lg_rows = lg[rows].cpu()
+    worst = (lg_rows - ref).abs().max().item()
+    draws = _check_draws(nxt, lg, temp, k, seed, 0, cfg.vocab_size)
+    for i in range(steps - 1):
+        t = tok[:, T0 + i]
+        print(f"  decode step {i} at position {T0 + i}", flush=True)
+        nxt, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), temp, k, seed=seed,
+                             step=i + 1, want_logits=True)
+        ref = R.forward(prep, t[rows, None], cache, last_only=True)[:, -1]
+        worst = max(worst, (lg[rows].cpu() - ref).abs().max().item())
+        draws += _check_draws(nxt, lg, temp, k, seed, i + 1, cfg.vocab_size)
+    eng.check_device()
+    return worst, draws
+
+
+def _check_draws(nxt, lg, temp, k, seed, step, V):
+    if temp == 0.0:
+        want = lg[:, :min(50257, V)].argmax(-1).to(torch.int32)
+        assert torch.equal(nxt, want), step
+        return nxt.numel()
+    lg = lg.cpu().numpy()
+    got = nxt.cpu().numpy()
+    for b in range(lg.shape[0]):
+        z = lg[b, :min(50257, V)]
+        assert int(got[b]) == _sample_small(z, temp, k, S.uniform(seed, step, b)), (step, b)
+    return lg.shape[0]
+
+
+def test_cfg3_shape_b64_prefill512_topk50():
+    """cfg3's shapes: d768 H6 x 128 at the full vocabulary (V = 50304, sampled
+    over 50257), 64 sequences, a 512-token prefill (one 512-query block), then
+    decode steps at 64 rows -- the skinny MFMA decode GEMMs at K = 768 and
+    33-64 rows, the decode attention at 64 x 6 heads, the top-k sampler over
+    the real vocabulary (1024 threads x 56 keys, partial last thread) at
+    T = 0.8, k = 50.  Three layers, layer 1 full-causal."""
+    cfg = GPTConfig(num_layers=3, num_heads=6, model_dim=768, seq_len=1024, window=384,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 51, dense=True))
+    print("case cfg3 shape: d768 L3 V50304 B=64 T0=512, T=0.8 top-k 50", flush=True)
+    worst, draws = _run_case(cfg, p, 64, 512, 4, [0, 29, 63], 0.8, 50, 2024, 1024)
+    assert worst < LOGIT_TOL, worst
+    assert draws == 64 * 4
+
+
+def test_cfg4_shape_ctx8192_b16():
+    """cfg4's shapes: the 155M dims at max_ctx 8192, 16 sequences, a
+    7680-token prefill (15 query blocks of 512; the windowed layers read 896
+    keys per block, the full layer all of them), then decode steps past 7680
+    where the full-causal layer reads every cached key.  Greedy."""
+    cfg = GPTConfig(num_layers=3, num_heads=6, model_dim=768, seq_len=8192, window=384,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 53, dense=True))
+    print("case cfg4 shape: d768 L3 ctx8192 B=16 T0=7680 greedy", flush=True)
+    worst, draws = _run_case(cfg, p, 16, 7680, 3, [0, 15], 0.0, 0, 0, 8192)
+    assert worst < LOGIT_TOL, worst
+
+
+def test_cfg5_shape_d1536_b128_topk50():
+    """cfg5's shapes: d1536 H12 x 128 at the full vocabulary, 128 sequences:
+    decode qkv / fc on the 64 x 64 MFMA tiles after the row norm, o / proj
+    on the LDS-staged skinny GEMM (proj K = 6144), the lm_head on the
+    128-row tiles, top-k 50 at T = 0.8 over 128 rows.  Three layers, layer 1
+    full-causal."""
+    cfg = GPTConfig(num_layers=3, num_heads=12, model_dim=1536, seq_len=256, window=384,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 55, dense=True))
+    print("case cfg5 shape: d1536 L3 V50304 B=128 T0=64, T=0.8 top-k 50", flush=True)
+    worst, draws = _run_case(cfg, p, 128, 64, 4, [0, 77, 127], 0.8, 50, 99, 256)
+    assert worst < LOGIT_TOL, worst
+    assert draws == 128 * 4
+
+
+def test_cfg1_degenerate_64_greedy_steps():
+    """cfg1 as specified (76.7M, model.py init: Wo = proj = x0 = 0), 16-token
+    prompt, all 64 greedy steps: every step repeats the last prompt token and
+    the logits equal the oracle's closed form."""
+    cfg = cfg_small_h4()
+    p = init_params(cfg, 0)
+    prompt = np.random.default_rng(1).integers(0, 50257, 16)
+    print("case cfg1: 76.7M degenerate init, 64 greedy steps", flush=True)
+    eng = _engine(cfg, p, 1, 128, 128)
+    got, glog = _greedy_gpu(eng, prompt, 64)
+    eng.check_device()
+    assert got == [int(prompt[-1])] * 64
+    ka = R.degenerate_known_answer(cfg, p, prompt[None, -1:])[0, -1]
+    assert max((g - ka).abs().max().item() for g in glog) < LOGIT_TOL
+
+
+def test_cfg1_dense_64_greedy_steps_match_oracle():
+    """cfg1's model with the dense init (Wo, proj drawn): 64 greedy steps
+    identical to the oracle's greedy decode, logits within tolerance."""
+    from tests.test_gpu_parity import _greedy_oracle
+    cfg = cfg_small_h4()
+    p = perturb_lambdas(init_params(cfg, 0, dense=True))
+    prompt = np.random.default_rng(1).integers(0, 50257, 16)
+    print("case cfg1 dense: 76.7M, 64 greedy steps vs oracle", flush=True)
+    eng = _engine(cfg, p, 1, 128, 128)
+    got, glog = _greedy_gpu(eng, prompt, 64)
+    eng.check_device()
+    ref, rlog = _greedy_oracle(cfg, p, prompt, 64)
+    n_same = next((i for i, (a, b) in enumerate(zip(got, ref)) if a != b), 64)
+    worst = max((g - r).abs().max().item() for g, r in zip(glog[:n_same], rlog[:n_same]))
+    assert worst < LOGIT_TOL, worst
+    assert got == ref, f"first divergence at step {n_same}"
+
+
+# ---- the drop-in API --------------------------------------------------------
+
+def test_sample_api_64_tokens_equals_engine_loop():
+    """sample() (ids kept on the device, streamed through pinned memory)
+    returns exactly what a plain prefill + decode loop on the engine draws,
+    for 64 top-k tokens of a batch of 3, and hands every step to on_token
+    in order."""
+    from attention_nn_amd.engine import Engine
+    from attention_nn_amd.sample import sample
+    cfg = GPTConfig(vocab_size=1000, num_layers=2, num_heads=2, model_dim=256, seq_len=96,
+                    window=16, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 61, dense=True))
+    p["lm_head"] = p["lm_head"] * 40
+    prompt = np.random.default_rng(62).integers(0, cfg.vocab_size, (3, 9))
+    seen = []
+    got = sample(prompt, 64, 0.9, 20, seed=7, params=p, cfg=cfg, on_token=seen.append)
+    eng = Engine(cfg, p, max_batch=3, max_ctx=96, max_tokens=3 * 96)
+    nxt, _ = eng.prefill(prompt, 0.9, 20, 7, 0)
+    want = [nxt.cpu().numpy()]
+    for i in range(1, 64):
+        nxt, _ = eng.decode(nxt, 0.9, 20, 7, i, out=nxt)
+        want.append(nxt.cpu().numpy())
+    want = np.stack(want, 1)
+    assert np.array_equal(np.asarray(got), want)
+    assert len(seen) == 64 and np.array_equal(np.stack(seen, 1), want)
+    # batch 1: the persistent step; a single prompt returns a list
+    one = sample(list(prompt[0]), 64, 0.0, 0, params=p, cfg=cfg)
+    eng1 = Engine(cfg, p, max_batch=1, max_ctx=96, max_tokens=96)
+    nxt, _ = eng1.prefill(prompt[:1])
+    ref = [int(nxt.item())]
+    for i in range(1, 64):
+        nxt, _ = eng1.decode(nxt, out=nxt)
+        ref.append(int(nxt.item()))
+    eng1.check_device()
+    assert one == ref
+
+
+def test_gpt_cache_repacks_on_new_params_not_on_growing_T():
+    """GPT.logits re-packs when an entry of the params dict is replaced and
+    not when the reference's loop calls it with a growing T."""
+    from attention_nn_amd.model import GPT
+    cfg = GPTConfig(vocab_size=512, num_layers=2, num_heads=2, model_dim=128, seq_len=64,
+                    window=16, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 63, dense=True))
+    tok = np.random.default_rng(64).integers(0, 512, (2, 40))
+    gpt = GPT(cfg)
+    for T in range(1, 40, 7):
+        a = gpt.logits(p, tok[:, :T])
+    assert gpt.packs == 1
+    ref = R.logits(cfg, p, tok[:, :T])
+    assert (a.cpu() - ref).abs().max().item() < LOGIT_TOL
+    p["lm_head"] = p["lm_head"] * 3          # same dict, new array
+    b = gpt.logits(p, tok[:, :T])
+    assert gpt.packs == 2
+    ref = R.logits(cfg, p, tok[:, :T])
+    assert (b.cpu() - ref).abs().max().item() < LOGIT_TOL
+    assert (a - b).abs().max().item() > 0.1
+    gpt.logits(p, tok[:1, :T])               # a smaller batch reuses the engine
+    assert gpt.packs == 2
+
+
+def test_sampling_state_greedy_after_sampled_and_more_rows():
+    """The device sampling state follows each call: a greedy call after a
+    sampled one at 12 rows (greedy then runs in the sampler kernel, which
+    reads the temperature from the device) returns the argmax; a sampled
+    call with more rows than the previous one draws every row with its own
+    (step, row) counter."""
+    cfg = GPTConfig(vocab_size=1000, num_layers=2, num_heads=2, model_dim=256, seq_len=64,
+                    window=16, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 65, dense=True))
+    p["lm_head"] = p["lm_head"] * 40
+    tok = np.random.default_rng(66).integers(0, cfg.vocab_size, (12, 7))
+    eng = _engine(cfg, p, 12, 64, 12 * 64)
+    print("case sampling state: 12 rows sampled -> greedy -> 4 rows -> 12 rows", flush=True)
+    nxt, lg = eng.prefill(tok, 0.8, 50, seed=3, step=0, want_logits=True)
+    _check_draws(nxt, lg, 0.8, 50, 3, 0, cfg.vocab_size)
+    nxt, lg = eng.prefill(tok, 0.0, 0, want_logits=True)
+    _check_draws(nxt, lg, 0.0, 0, 0, 0, cfg.vocab_size)
+    nxt, lg = eng.prefill(tok[:4], 0.9, 10, seed=4, step=5, want_logits=True)
+    _check_draws(nxt, lg, 0.9, 10, 4, 5, cfg.vocab_size)
+    nxt, lg = eng.prefill(tok, 0.9, 10, seed=4, step=6, want_logits=True)
+    _check_draws(nxt, lg, 0.9, 10, 4, 6, cfg.vocab_size)
+    for i in range(3):
+        nxt, lg = eng.decode(nxt, 0.9, 10, seed=4, step=7 + i, want_logits=True)
+        _check_draws(nxt, lg, 0.9, 10, 4, 7 + i, cfg.vocab_size)
