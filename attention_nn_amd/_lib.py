@@ -73,6 +73,8 @@ SIGNATURES = {
     "ann_op_polar_express": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _SZ, _P]),
     "ann_op_normuon_ws_bytes": (ctypes.c_size_t, [_I, _I, _I]),
     "ann_op_normuon": (ctypes.c_int, [_P, _P, _I, _I, _I, _F, _P, _P, _SZ, _P]),
+    "ann_op_normuon_noalloc_max_bytes": (ctypes.c_size_t, []),
+    "ann_op_normuon_noalloc": (ctypes.c_int, [_P, _P, _I, _I, _I, _F, _P, _P]),
     "ann_profile_enable": (ctypes.c_int, [_P, _I, _I]),
     "ann_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(_I)]),
     "ann_check_device": (ctypes.c_int, [_P, _P]),

@@ -1002,4 +1002,25 @@ int ann_op_normuon(const void* v, float* second_mom, int32_t batch, int32_t M, i
   return ANN_OK;
 }
 
+size_t ann_op_normuon_noalloc_max_bytes(void) { return NM_SCRATCH_BYTES; }
+
+int ann_op_normuon_noalloc(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
+                           float beta2, float* out, void* stream) {
+  if (!v || !second_mom || !out) return fail(ANN_E_ARG, "null argument");
+  if (batch <= 0 || M <= 0 || N <= 0)
+    return fail(ANN_E_ARG, "bad shape batch=%d M=%d N=%d", batch, M, N);
+  const size_t need = normuon_ws_bytes(batch, M, N);
+  if (need > NM_SCRATCH_BYTES)
+    return fail(ANN_E_CAPACITY,
+                "normuon_noalloc: scratch of %zu bytes needed, the fixed array holds %zu "
+                "(batch * max(M, N) up to %zu)",
+                need, NM_SCRATCH_BYTES, NM_SCRATCH_BYTES / 8);
+  const hipError_t e = normuon_noalloc((const bf16_t*)v, second_mom, batch, M, N, beta2, out,
+                                       (hipStream_t)stream);
+  if (e == hipErrorInvalidDevice)
+    return fail(ANN_E_ARG, "normuon_noalloc: the stream must belong to the current device");
+  if (e != hipSuccess) return fail(ANN_E_HIP, "normuon_noalloc: %s", hipGetErrorString(e));
+  return ANN_OK;
+}
+
 }  // extern "C"

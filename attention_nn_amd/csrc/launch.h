@@ -113,6 +113,12 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
 size_t normuon_ws_bytes(int batch, int M, int N);
 hipError_t normuon(const bf16_t* v, float* second_mom, int batch, int M, int N, float beta2,
                    float* out, void* ws, size_t ws_bytes, hipStream_t st);
+// NorMuon with its scratch in a fixed device array of NM_SCRATCH_BYTES (no
+// allocation; calls that overlap on one GPU race); normuon_ws_bytes(batch, M,
+// N) must not exceed it.
+constexpr size_t NM_SCRATCH_BYTES = (size_t)4 << 20;
+hipError_t normuon_noalloc(const bf16_t* v, float* second_mom, int batch, int M, int N,
+                           float beta2, float* out, hipStream_t st);
 // Per-row loss = log(sum over tiles of ce_part) - ce_tz (tiles summed in
 // order), written to rows[M]; mean over the rows (fixed order) to *mean.
 hipError_t ce_finalize(const float* part, int ld, int ntiles, const float* tz, int M, float* rows,

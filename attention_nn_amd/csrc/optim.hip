@@ -17,6 +17,7 @@
 // All reductions run in a fixed order: results are bit-reproducible.
 #include <math.h>
 #include <string.h>
+#include <mutex>
 #include "common.h"
 #include "launch.h"
 
@@ -426,6 +427,56 @@ hipError_t muon_apply(const float* p, const float* u, size_t n, float lr, float 
   if (!n) return hipSuccess;
   hipLaunchKernelGGL(k_muon_apply, dim3(grid_for(n, 256)), dim3(256), 0, st, p, u, n, lr, wd, po);
   return hipGetLastError();
+}
+
+}  // namespace ann
+
+// ---- NorMuon without an allocation ------------------------------------------
+// The scratch of normuon_noalloc (the (batch, R) means and scales) lives in a
+// file-scope device array of fixed size: every GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, not a device address: its address on the current device
+// comes from hipGetSymbolAddress, taken once per device with that device
+// current, and only that pointer is handed to the kernels.  Every call on one
+// GPU shares its array (NorMuon writes all of it before reading it, so nothing
+// needs clearing); calls that overlap on one GPU race.
+static __device__ __align__(256) unsigned char scratch[ann::NM_SCRATCH_BYTES];
+
+namespace ann {
+namespace {
+constexpr int NM_MAX_DEVICES = 64;
+std::mutex g_nm_mu;
+void* g_nm_scratch[NM_MAX_DEVICES];   // device address of `scratch`, per device
+}  // namespace
+
+// Device address of this GPU's scratch array; the stream must belong to the
+// current device.
+hipError_t normuon_scratch(hipStream_t st, void** out) {
+  int dev = -1, sdev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  e = hipStreamGetDevice(st, &sdev);
+  if (e != hipSuccess) return e;
+  if (dev != sdev || dev < 0 || dev >= NM_MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_nm_mu);
+  if (!g_nm_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_nm_scratch[dev] = p;
+  }
+  *out = g_nm_scratch[dev];
+  return hipSuccess;
+}
+
+hipError_t normuon_noalloc(const bf16_t* v, float* second_mom, int batch, int M, int N,
+                           float beta2, float* out, hipStream_t st) {
+  if (normuon_ws_bytes(batch, M, N) > NM_SCRATCH_BYTES) return hipErrorInvalidValue;
+  void* ws = nullptr;
+  const hipError_t e = normuon_scratch(st, &ws);
+  if (e != hipSuccess) return e;
+  return normuon(v, second_mom, batch, M, N, beta2, out, ws, NM_SCRATCH_BYTES, st);
 }
 
 }  // namespace ann

@@ -221,6 +221,20 @@ size_t ann_op_normuon_ws_bytes(int32_t batch, int32_t M, int32_t N);
 int ann_op_normuon(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
                    float beta2, float* out, void* ws, size_t ws_bytes, void* stream);
 
+/* NorMuon without an allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight training or serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as ann_op_normuon, minus the workspace: the scratch
+ * is a fixed device array of ann_op_normuon_noalloc_max_bytes() (4 MiB) inside
+ * the library, one per GPU, held until the process ends, so batch * max(M, N)
+ * may be at most 524288 (ANN_E_CAPACITY beyond).  The function itself calls
+ * no hipMalloc / hipFree.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams or threads) race.  The stream
+ * must belong to the current device. */
+size_t ann_op_normuon_noalloc_max_bytes(void);
+int ann_op_normuon_noalloc(const void* v, float* second_mom, int32_t batch, int32_t M, int32_t N,
+                           float beta2, float* out, void* stream);
+
 /* Device status of the decode steps (no reference counterpart).  The
  * cross-work-group waits of the persistent batch-1 step and of the decode
  * attention's split combine are bounded; one that gives up sets a device flag
