@@ -203,6 +203,9 @@ struct ann_ctx {
   // the next projections' weights ahead; -1 = not read yet, -2 = sized by
   // bytes, >= 0 = fixed by ANN_PREFETCH_WG
   int pf_wgs = -1;
+  // decode attention: splits per (row, head) fixed by ANN_DEC_SPLITS (0: sized
+  // by the batch, about 384 work-groups)
+  int dec_split_env = 0;
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -284,11 +287,12 @@ int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* 
 // 64), at most one 64-key chunk per split of the longest key range.
 // Independent of the current length, so a captured step replays at every
 // position.
-int dec_splits(const ann_config& g, bool lng, int B) {
+int dec_splits(const ann_ctx* c, bool lng, int B) {
+  const ann_config& g = c->c;
   const int keys = lng ? g.max_ctx : (g.window < g.max_ctx ? g.window : g.max_ctx);
   int n = (keys + 63) / 64;
   if (n > MAX_SPLIT) n = MAX_SPLIT;
-  const int want = (384 + B * g.H - 1) / (B * g.H);
+  const int want = c->dec_split_env > 0 ? c->dec_split_env : (384 + B * g.H - 1) / (B * g.H);
   if (n > want) n = want;
   return n < 1 ? 1 : n;
 }
@@ -366,7 +370,7 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
     er.ldr = d;
     er.lam = lam + 8 * l;
     if (T == 1) {  // decode: fused QK-norm / RoPE / KV append and split combine
-      const int ns = dec_splits(g, lng, B);
+      const int ns = dec_splits(c, lng, B);
       // while the attention streams the KV cache, extra work-groups read this
       // layer's o / fc / proj weights and the next layer's qkv (contiguous
       // from o) so the projections find them in the memory-side cache
@@ -654,6 +658,9 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->use_graph = !(ge && ge[0] == '0');
   const char* pe = getenv("ANN_PERSIST");
   c->pd_env = !(pe && pe[0] == '0');
+  const char* ds = getenv("ANN_DEC_SPLITS");
+  c->dec_split_env = ds ? atoi(ds) : 0;
+  if (c->dec_split_env < 0 || c->dec_split_env > MAX_SPLIT) c->dec_split_env = 0;
   const char* pc = getenv("ANN_PERSIST_COOP");
   c->pd_coop = pc && pc[0] == '1';
   *out = c;
@@ -898,7 +905,11 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
     HIPCHK(hipMemsetAsync(c->ws + c->sl.acnt, 0, (size_t)c->c.max_batch * c->c.H * 4, st));
     c->dec_clear = false;
   }
-  if (c->use_graph && c->prof_kind < 0)
+  // The batch-1 persistent step is one kernel (plus the sampler when not
+  // greedy): launched directly, measured 2.5% more tokens per second than
+  // replaying it as a graph (0.2019 against 0.2070 ms per token at 155M).
+  // The per-kernel path (tens of launches) replays its captured graph.
+  if (c->use_graph && c->prof_kind < 0 && !persist_ok(c, B))
     rc = decode_graph(c, tokens, B, greedy, out_tok, logits, st);
   else
     rc = enqueue_decode(c, tokens, B, greedy, out_tok, logits, st);

@@ -15,12 +15,11 @@ the decode-only rate are reported beside it.
 
 roofline: the dominant kernel -- at batch 1 the whole decode step is one
 persistent kernel (k_decode_persist: embed, every layer, lm_head + softcap,
-greedy argmax in one launch).  Timed steps replay it from a HIP graph, where
-events cannot bracket it, so one more generation launches it eagerly with a
-HIP event pair around every launch on its stream (991 launches, positions
-32..1022); achieved = the mean algorithmic bytes of a step (bf16 weights
-once, K/V rows read and appended, embedding row) / the mean launch time,
-against the 8 TB/s peak.
+greedy argmax in one launch), launched directly once per token.  One more
+generation brackets every launch with a HIP event pair on its stream (991
+launches, positions 32..1022); achieved = the mean algorithmic bytes of a
+step (bf16 weights once, K/V rows read and appended, embedding row) / the
+mean bracketed launch time, against the 8 TB/s peak.
 
 Every pass ends with the device check of the persistent step's bounded waits
 (a step that gave up would end early and inflate the rate); the run exits
@@ -425,13 +424,13 @@ def main():
         check(eng, "trace run")
         print(f"trace run: prefill {prompt_len} + {n_decode} greedy decode steps", flush=True)
         return 0
-    # timed: K whole generations; each decode step replays one captured HIP
-    # graph (one launch of the persistent step kernel per token)
+    # timed: K whole generations; each decode step is one launch of the
+    # persistent step kernel
     total_ms, gen, dec = timed_generations(eng, prompt, n_decode, args.steps, args.warmup,
                                            0.0, 0, 0)
     check(eng, "the timed generations")
     # roofline: one more generation, every step kernel launch bracketed by
-    # events on its stream (eager launches; events cannot sit in a graph)
+    # events on its stream
     k_ms, k_n = step_kernel_times(eng, prompt, n_decode)
     check(eng, "the roofline generation")
     gen_tokens = n_decode + 1
