@@ -36,7 +36,9 @@ def flatten_opt_state(state):
         for k, v in st.items():
             if "|" in k:
                 raise ValueError(f"optimizer state key {k!r} of {name!r} contains '|'")
-            flat[f"{name}|{k}"] = np.ascontiguousarray(np.asarray(v))
+            # order="C" keeps 0-d arrays 0-d (the step counter "_step|t" is a
+            # 0-d array in the reference's files); ascontiguousarray would not
+            flat[f"{name}|{k}"] = np.asarray(v, order="C")
     return flat
 
 

@@ -23,7 +23,8 @@ namespace ann {
 //                   the tile holding the target (metal_kernels.py:153-193)
 //   EPI_PE_B        (Polar Express) out = bf16(bf16(s0*x) + bf16(s1*bf16(y)))  (muon.py:37)
 //   EPI_PE_X        (Polar Express) out = bf16(bf16(s0*x) + bf16(y))           (muon.py:38,42)
-//                   x is the epilogue's second operand (M, ldr)
+//                   x is the epilogue's second operand (M, ldr); when outT is set
+//                   the same values also go to outT (N, ldoT), transposed
 enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4,
        EPI_QKV = 5, EPI_CE = 6, EPI_PE_B = 7, EPI_PE_X = 8 };
 
@@ -57,6 +58,9 @@ struct EpiArgs {
   const int32_t* tgt;
   // PE_B / PE_X scalars
   float s0, s1;
+  // PE_X: transposed copy of the output, or null
+  bf16_t* outT;
+  int ldoT;
 };
 
 // Sampling parameters read by the sampler from device memory (so a captured

@@ -51,7 +51,9 @@ __device__ __forceinline__ void epilogue(const EpiArgs& ea, int m, int n, float 
     ea.out[(size_t)m * ea.ldo + n] = f2bf(rbf(ea.s0 * bf2f(ea.x[i])) + rbf(ea.s1 * rbf(y)));
   } else if (EPI == EPI_PE_X) {
     const size_t i = (size_t)m * ea.ldr + n;
-    ea.out[(size_t)m * ea.ldo + n] = f2bf(rbf(ea.s0 * bf2f(ea.x[i])) + rbf(y));
+    const bf16_t o = f2bf(rbf(ea.s0 * bf2f(ea.x[i])) + rbf(y));
+    ea.out[(size_t)m * ea.ldo + n] = o;
+    if (ea.outT) ea.outT[(size_t)n * ea.ldoT + m] = o;
   } else {  // EPI_LOGITS
     const bf16_t z = f2bf(y);
     const size_t i = (size_t)m * ea.ldz + n;
@@ -117,6 +119,12 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, bool vec, int m, in
       o[r] = EPI == EPI_PE_B ? rbf(ea.s0 * xf[r]) + rbf(ea.s1 * rbf(y[r]))
                              : rbf(ea.s0 * xf[r]) + rbf(y[r]);
     *(uint2*)(ea.out + (size_t)m * ea.ldo + n) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+    // transposed copy: 2-byte stores, consecutive m across the 16 lanes of a
+    // group, so each column's stores coalesce into one 32-byte run
+    if (EPI == EPI_PE_X && ea.outT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ea.outT[(size_t)(n + r) * ea.ldoT + m] = f2bf(o[r]);
+    }
   } else {  // EPI_LOGITS
     bf16_t z[4];
 #pragma unroll
@@ -741,6 +749,7 @@ __global__ __launch_bounds__(256) void k_gemm_bat(const bf16_t* __restrict__ A, 
   const long long z = blockIdx.z;
   ea.out += z * sOut;
   ea.x += z * sX;
+  if (ea.outT) ea.outT += z * sOut;   // same shape as out
   gemm_body<EPI, BM, GM_BN>(A + z * sA, lda, W + z * sW, M, N, K, ea);
 }
 

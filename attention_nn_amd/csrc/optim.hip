@@ -187,7 +187,7 @@ size_t polar_express_ws_bytes(int batch, int M, int N) {
   if (batch <= 0 || M <= 0 || N <= 0) return 0;
   const size_t mn = (size_t)M * N, S = M < N ? M : N;
   const size_t nch = (mn + PE_CHUNK - 1) / PE_CHUNK;
-  return up256(batch * mn * 2) * 2 + up256(batch * S * S * 2) * 2 + up256(batch * nch * 4) +
+  return up256(batch * mn * 2) * 3 + up256(batch * S * S * 2) * 2 + up256(batch * nch * 4) +
          up256(batch * 4);
 }
 
@@ -200,7 +200,8 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
   const int nch = (int)((mn + PE_CHUNK - 1) / PE_CHUNK);
   char* w = (char*)ws;
   bf16_t* xb = (bf16_t*)w;  w += up256(batch * mn * 2);    // the other x buffer
-  bf16_t* xt = (bf16_t*)w;  w += up256(batch * mn * 2);    // x^T
+  bf16_t* xt = (bf16_t*)w;  w += up256(batch * mn * 2);    // x^T of the current x
+  bf16_t* xt2 = (bf16_t*)w; w += up256(batch * mn * 2);    // x^T of the next x
   bf16_t* am = (bf16_t*)w;  w += up256(batch * S * S * 2); // A
   bf16_t* bm = (bf16_t*)w;  w += up256(batch * S * S * 2); // B
   float* part = (float*)w;  w += up256(batch * (size_t)nch * 4);
@@ -215,13 +216,15 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
   bf16_t* nxt = out;
   const bool tall = M > N;
   const dim3 tg((N + TR_T - 1) / TR_T, (M + TR_T - 1) / TR_T, batch);
+  // x^T of the first x by a transpose; each iteration's x' = a x + B x
+  // epilogue also writes x'^T for the next one (the last one's is not needed)
+  hipLaunchKernelGGL(k_transpose_bf16, tg, dim3(256), 0, st, cur, xt, M, N);
   for (int it = 0; it < 5; ++it) {
     const float a = bf16_round_host(PE_COEF[it][0]);
     const float b = bf16_round_host(PE_COEF[it][1]);
     const float c = bf16_round_host(PE_COEF[it][2]);
     EpiArgs ea{};
     hipError_t e;
-    hipLaunchKernelGGL(k_transpose_bf16, tg, dim3(256), 0, st, cur, xt, M, N);
     if (!tall) {
       // A = x x^T (M x M, K = N)
       ea.out = am;
@@ -244,6 +247,8 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
       ea.x = cur;
       ea.ldr = N;
       ea.s0 = a;
+      ea.outT = it < 4 ? xt2 : nullptr;
+      ea.ldoT = M;
       e = gemm_batched(EPI_PE_X, bm, M, (long long)S * S, xt, (long long)mn, M, N, M, ea,
                        (long long)mn, (long long)mn, batch, st);
       if (e != hipSuccess) return e;
@@ -268,6 +273,8 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
       ea.x = cur;
       ea.ldr = N;
       ea.s0 = a;
+      ea.outT = it < 4 ? xt2 : nullptr;
+      ea.ldoT = M;
       e = gemm_batched(EPI_PE_X, cur, N, (long long)mn, bm, (long long)S * S, M, N, N, ea,
                        (long long)mn, (long long)mn, batch, st);
       if (e != hipSuccess) return e;
@@ -275,6 +282,9 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
     bf16_t* t = cur;
     cur = nxt;
     nxt = t;
+    t = xt;
+    xt = xt2;
+    xt2 = t;
   }
   return hipGetLastError();
 }

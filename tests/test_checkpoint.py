@@ -77,3 +77,18 @@ def test_shape_and_name_checks(tmp_path, small):
     wrong["fc_bank"]["v"] = np.zeros((1,), np.float32)
     with pytest.raises(ValueError, match="shape mismatch for fc_bank"):       # muon.py:156
         C.load_checkpoint(save, p, wrong)
+
+
+def test_zero_d_state_keeps_its_shape(tmp_path):
+    """The optimizer's step counter is a 0-d array ("_step|t", muon.py:143):
+    written and read back it stays 0-d, as a reference file holds it."""
+    from safetensors.numpy import load_file, save_file
+    st = {"_step": {"t": np.array(3.0, dtype=np.float32)},
+          "embed": {"m": np.zeros((2, 3), np.float32)[:, ::2]}}     # non-contiguous too
+    flat = C.flatten_opt_state(st)
+    assert flat["_step|t"].shape == ()
+    assert flat["embed|m"].flags.c_contiguous and flat["embed|m"].shape == (2, 2)
+    path = str(tmp_path / "s.opt.safetensors")
+    save_file(flat, path)
+    back = C.unflatten_opt_state(load_file(path), st)
+    assert back["_step"]["t"].shape == () and float(back["_step"]["t"]) == 3.0

@@ -103,3 +103,31 @@ def test_muon_adam_steps_match_oracle():
             # the update is what the step computes: compare against its size
             assert d <= 0.05 * scale + 1e-7, (step, k, d, scale)
     assert float(gpu.state["_step"]["t"].item()) == 3.0
+
+
+def test_muon_adam_state_resume(tmp_path):
+    """Optimizer state written after two steps and read into a new MuonAdam
+    resumes exactly: the step counter (kept on the host during steps) comes
+    back from the file, and the third step equals an uninterrupted one."""
+    from attention_nn_amd import optim as G
+    from attention_nn_amd.config import GPTConfig
+    from attention_nn_amd.weights import init_params
+    cfg = GPTConfig(vocab_size=192, num_layers=1, num_heads=2, model_dim=64, seq_len=32,
+                    window=16, long_layers=(0,))
+    p0 = {k: torch.from_numpy(v).cuda() for k, v in init_params(cfg, 4, dense=True).items()}
+    rng = np.random.default_rng(12)
+    grads = [{k: torch.from_numpy(rng.standard_normal(v.shape).astype(np.float32) * 0.01).cuda()
+              for k, v in p0.items()} for _ in range(3)]
+    a = G.MuonAdam(p0, G.optimizer_table())
+    p = p0
+    for gr in grads[:2]:
+        p = a(p, gr)
+    a.save_state(str(tmp_path / "s.opt.safetensors"))
+    b = G.MuonAdam(p0, G.optimizer_table())
+    b.load_state(str(tmp_path / "s.opt.safetensors"))
+    assert b._t == 2.0
+    pa = a(p, grads[2])
+    pb = b(p, grads[2])
+    for k in p0:
+        assert torch.equal(pa[k], pb[k]), k
+    assert float(b.state["_step"]["t"].item()) == 3.0
