@@ -1,0 +1,322 @@
+// Large projections y = a @ W^T (W stored (N, K) bf16) of the prefill and the
+// training forward: 256 x 256 output tiles of four waves of 128 x 128, one work-
+// group (one wave per SIMD) per CU, v_mfma_f32_16x16x32_bf16.  The projection
+// routing sends the fc (relu^2) and o-proj (attention residual) projections
+// here (see gemm_big_routes for the measurements); it serves the plain, MLP
+// residual and QKV epilogues as well when called directly.
+//
+// Main loop (K tiles of 64, two LDS stages, one barrier per K tile):
+//   * the 256 accumulators of a wave live in AGPRs: the MFMA is issued as
+//     inline assembly whose accumulator operand is an AGPR ("+a").  With the
+//     compiler builtin the accumulators move between AGPRs and VGPRs inside the
+//     loop (368 v_accvgpr moves per K tile, measured ~10% slower);
+//   * the fragments are read with volatile inline ds_read_b128 in a fixed
+//     order -- the first k-step's eight W fragments and the first A fragment,
+//     then the second k-step's W fragments -- and each A fragment one group of
+//     eight MFMAs ahead of its use, with hand-placed s_waitcnt (the compiler's
+//     scheduler otherwise reads every A fragment right before its MFMAs and
+//     waits for it);
+//   * each of the 16 MFMA groups of a K tile first stores one 16-byte chunk per
+//     thread of the next K tile into the other LDS stage and refills that
+//     register with the tile after it, so the tile traffic hides behind the
+//     MFMAs.  All of these are unconditional (past the last K tile they re-read
+//     it and fill the stage no later iteration reads): a branch there makes the
+//     compiler wait on every load in flight.  The prologue issues the second
+//     tile's loads in the loop's order, so the loop's waits stay vmcnt(15).
+//   * LDS tiles are unpadded 128-byte rows with chunk c of row r at slot
+//     c ^ ((r >> 1) & 7): conflict-free for the chunk stores and the
+//     16-row fragment reads.
+// The MFMA operands are swapped (C^T = W A^T) so that a lane holds four
+// consecutive columns of one row.  Epilogue: the tile is rounded to bf16 (every
+// epilogue here starts from bf16(y), as the reference's eager ops do) into LDS
+// (row pitch 264: the 8-byte writes of 16 rows spread over the banks), then
+// each thread handles 16-byte row chunks: plain / relu^2 stores, the residual
+// mixes (x, x0 read and x written as 16-byte words), or the QKV epilogue of
+// each 128-column half (QK-norm, RoPE, q and KV-cache writes).  Work-group i
+// runs on XCD i % 8; each XCD takes a contiguous range of tiles, N-fastest, so
+// the N tiles of an M block share its A rows in that XCD's L2.
+// Measured against the four prefill shapes (M = 32768) with a plain store:
+// 0.81 / 0.70 / 0.96 / 1.04 PFLOP/s for N x K = 2304 x 768, 768 x 768,
+// 3072 x 768, 768 x 3072 (hipBLASLt: 0.87 / 0.83 / 1.17 / 1.29).
+#include <type_traits>
+#include "common.h"
+#include "epilogue.h"
+#include "launch.h"
+
+namespace ann {
+
+namespace {
+
+constexpr int BG_BM = 256, BG_BN = 256, BG_BK = 64;
+constexpr int BG_EP = 264;   // bf16 row pitch of the staged output tile
+constexpr size_t BG_LDS_MAIN = (size_t)2 * (BG_BM + BG_BN) * BG_BK * 2;
+constexpr size_t BG_LDS_EPI = (size_t)BG_BM * BG_EP * 2;
+constexpr size_t BG_LDS = BG_LDS_MAIN > BG_LDS_EPI ? BG_LDS_MAIN : BG_LDS_EPI;
+
+typedef __bf16 bg_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float bg_floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned bg_u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char bg_lds_char;
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void bg_static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    bg_static_for<I + 1, N>(f);
+  }
+}
+
+__device__ __forceinline__ int bg_off(int r, int c) { return r * BG_BK + ((c ^ ((r >> 1) & 7)) << 3); }
+
+__device__ __forceinline__ void bg_mfma(bg_floatx4& acc, const bg_bf16x8& a, const bg_bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int OFF>
+__device__ __forceinline__ bg_bf16x8 bg_lds_read(const bg_lds_char* p) {
+  bg_bf16x8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(p), "i"(OFF));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void bg_wait_lgkm() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t bg_pack_bf16(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+}  // namespace
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, const bf16_t* W,
+                                                     int M, int N, int K, EpiArgs ea) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  auto As = [&](int s) { return smem + s * BG_BM * BG_BK; };
+  auto Ws = [&](int s) { return smem + 2 * BG_BM * BG_BK + s * BG_BN * BG_BK; };
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int ntm = (M + BG_BM - 1) / BG_BM, ntn = N / BG_BN, nt = ntm * ntn;
+  const int per = (nt + 7) / 8;
+  const int t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (t >= nt) return;
+  const int tm = t / ntn, tn = t % ntn;
+  const int m0 = tm * BG_BM, n0 = tn * BG_BN;
+  const int KT = K / BG_BK;
+
+  // staged K-tile chunks: chunk g of a thread is operand g & 1 (A, W), row
+  // block g >> 1 (rows (tid >> 3) + 32 u), 16-byte column tid & 7
+  bg_u32x4 ra[8], rw[8];
+  const int crow = tid >> 3, cc = tid & 7;
+  auto gload1 = [&](int op, int u, int kt) {
+    const int row = crow + 32 * u;
+    if (op == 0)
+      ra[u] = *(const bg_u32x4*)(A + (size_t)min(m0 + row, M - 1) * lda + kt * BG_BK + cc * 8);
+    else
+      rw[u] = *(const bg_u32x4*)(W + (size_t)(n0 + row) * K + kt * BG_BK + cc * 8);
+  };
+  auto lstore1 = [&](int op, int u, int s) {
+    const int row = crow + 32 * u;
+    if (op == 0) *(bg_u32x4*)(As(s) + bg_off(row, cc)) = ra[u];
+    else *(bg_u32x4*)(Ws(s) + bg_off(row, cc)) = rw[u];
+  };
+
+  bg_floatx4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = (bg_floatx4){0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, kg = lane >> 4;
+
+  // prologue: tile 0 into stage 0, tile 1 (clamped) in flight in the
+  // loop's order, each load pinned in place
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    gload1(0, u, 0);
+    gload1(1, u, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    lstore1(0, u, 0);
+    lstore1(1, u, 0);
+  }
+  bg_static_for<0, 16>([&](auto gc) __attribute__((always_inline)) {
+    constexpr int g = decltype(gc)::value;
+    gload1(g & 1, g >> 1, min(1, KT - 1));
+    asm volatile("" ::: "memory");
+  });
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt & 1;
+    const bf16_t* as = As(s) + (wm * 128 + r16) * BG_BK;
+    const bf16_t* ws = Ws(s) + (wn * 128 + r16) * BG_BK;
+    const int ch0 = kg ^ ((r16 >> 1) & 7), ch1 = (4 + kg) ^ ((r16 >> 1) & 7);
+    const bg_lds_char* pa0 = (const bg_lds_char*)(as + (ch0 << 3));
+    const bg_lds_char* pa1 = (const bg_lds_char*)(as + (ch1 << 3));
+    const bg_lds_char* pb0 = (const bg_lds_char*)(ws + (ch0 << 3));
+    const bg_lds_char* pb1 = (const bg_lds_char*)(ws + (ch1 << 3));
+    bg_bf16x8 b0[8], b1[8];
+    bg_static_for<0, 8>([&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      b0[j] = bg_lds_read<j * 16 * BG_BK * 2>(pb0);
+    });
+    bg_bf16x8 a = bg_lds_read<0>(pa0);
+    bg_static_for<0, 8>([&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      b1[j] = bg_lds_read<j * 16 * BG_BK * 2>(pb1);
+    });
+    bg_wait_lgkm<8>();   // b0 and a; the eight b1 reads may still fly
+    bg_static_for<0, 16>([&](auto gc) __attribute__((always_inline)) {
+      constexpr int g = decltype(gc)::value;
+      constexpr int i = g & 7, kh = g >> 3;
+      bg_bf16x8 an = a;
+      if constexpr (g < 15) {
+        constexpr int ni = (g + 1) & 7;
+        an = ((g + 1) >> 3) ? bg_lds_read<ni * 16 * BG_BK * 2>(pa1)
+                            : bg_lds_read<ni * 16 * BG_BK * 2>(pa0);
+      }
+      lstore1(g & 1, g >> 1, s ^ 1);
+      gload1(g & 1, g >> 1, min(kt + 2, KT - 1));
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bg_mfma(acc[i][j], kh ? b1[j] : b0[j], a);
+      if constexpr (g < 15) bg_wait_lgkm<0>();
+      a = an;
+    });
+    __syncthreads();
+  }
+
+  // ---- stage bf16(y): lane holds row m = block row + r16, columns 4 kg ..
+  bf16_t* st = smem;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int ml = wm * 128 + i * 16 + r16, nl = wn * 128 + j * 16 + 4 * kg;
+      const bg_floatx4 v = acc[i][j];
+      *(uint2*)(st + ml * BG_EP + nl) = make_uint2(bg_pack_bf16(v[0], v[1]), bg_pack_bf16(v[2], v[3]));
+    }
+  __syncthreads();
+
+  if constexpr (EPI == EPI_QKV) {
+    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st, m0, n0, M, tid);
+    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st + 128, m0, n0 + 128, M, tid);
+    return;
+  } else {
+    // 16-byte row chunks: chunk q = tid + 256 u is row q >> 5, columns 8 (q & 31)
+#pragma unroll 4
+    for (int u = 0; u < 32; ++u) {
+      const int q = tid + 256 * u;
+      const int ml = q >> 5, c8 = (q & 31) * 8;
+      const int m = m0 + ml, n = n0 + c8;
+      if (m >= M) continue;
+      const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
+      const uint2 hi = *(const uint2*)(st + ml * BG_EP + c8 + 4);
+      const uint32_t yw[4] = {lo.x, lo.y, hi.x, hi.y};
+      if constexpr (EPI == EPI_STORE) {
+        *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      } else if constexpr (EPI == EPI_RELU2) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (uint32_t)relu2_bf(__uint_as_float(yw[e] << 16)) |
+                 ((uint32_t)relu2_bf(__uint_as_float(yw[e] & 0xffff0000u)) << 16);
+        *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {   // EPI_RESID_ATTN / EPI_RESID_MLP
+        const size_t i = (size_t)m * ea.ldr + n;
+        const uint4 xv = *(const uint4*)(ea.x + i);
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        uint32_t zw[4] = {0u, 0u, 0u, 0u};
+        if constexpr (EPI == EPI_RESID_ATTN) {
+          const uint4 zv = *(const uint4*)(ea.x0 + i);
+          zw[0] = zv.x; zw[1] = zv.y; zw[2] = zv.z; zw[3] = zv.w;
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bf16_t r[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float xf = __uint_as_float(h ? (xw[e] & 0xffff0000u) : (xw[e] << 16));
+            const float yf = __uint_as_float(h ? (yw[e] & 0xffff0000u) : (yw[e] << 16));
+            if constexpr (EPI == EPI_RESID_ATTN) {
+              const float zf = __uint_as_float(h ? (zw[e] & 0xffff0000u) : (zw[e] << 16));
+              r[h] = mix_attn(ea.lam, xf, zf, yf);
+            } else {
+              r[h] = mix_mlp(ea.lam, xf, yf);
+            }
+          }
+          o[e] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+        }
+        *(uint4*)(ea.x + i) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
+// Whether the projection routing (gemm()) sends (epi, M, N, K) here.  In the
+// 64 x 512-token prefill, against the two-work-groups-per-CU tiles of
+// k_gemm_2w (rocprof): fc (relu^2) 182 against 190 us and o-proj (attention
+// residual) 103 against 108 us go here; qkv (170 against 151 us) and proj
+// (MLP residual, 197 against 193 us) do not -- with one work-group per CU the
+// heavier epilogues (QK-norm / RoPE / cache writes, x read and written) are
+// not overlapped by another work-group's MFMAs.  The kernel still serves
+// every epilogue of gemm_big() when called directly.
+bool gemm_big_routes(int epi) { return epi == EPI_RELU2 || epi == EPI_RESID_ATTN; }
+
+// Whether gemm_big can take (epi, M, N, K): whole 256-column tiles, 64-deep K
+// tiles, 16-byte aligned rows and outputs, and enough tiles (at least 96) for
+// the one-work-group-per-CU kernel to fill the chip.
+bool gemm_big_fits(int epi, const bf16_t* A, int lda, int M, int N, int K, const EpiArgs& ea) {
+  if (M < 512 || N % BG_BN || K % BG_BK || K < BG_BK || lda % 8 || ((uintptr_t)A & 15)) return false;
+  if ((long long)((M + BG_BM - 1) / BG_BM) * (N / BG_BN) < 96) return false;
+  switch (epi) {
+    case EPI_STORE:
+    case EPI_RELU2:
+      return ea.out && ea.ldo % 8 == 0 && ((uintptr_t)ea.out & 15) == 0;
+    case EPI_RESID_ATTN:
+      return ea.x && ea.x0 && ea.lam && ea.ldr % 8 == 0 &&
+             (((uintptr_t)ea.x | (uintptr_t)ea.x0) & 15) == 0;
+    case EPI_RESID_MLP:
+      return ea.x && ea.lam && ea.ldr % 8 == 0 && ((uintptr_t)ea.x & 15) == 0;
+    case EPI_QKV:
+      return true;   // gemm_qkv_fits has been checked by the caller
+    default:
+      return false;
+  }
+}
+
+template <int EPI>
+static hipError_t launch_big(const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                             const EpiArgs& ea, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_big<EPI>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)BG_LDS);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const int nt = ((M + BG_BM - 1) / BG_BM) * (N / BG_BN);
+  const int grid = (nt + 7) / 8 * 8;
+  hipLaunchKernelGGL(k_gemm_big<EPI>, dim3(grid), dim3(256), BG_LDS, st, A, lda, W, M, N, K, ea);
+  return hipGetLastError();
+}
+
+hipError_t gemm_big(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                    const EpiArgs& ea, hipStream_t st) {
+  if (!gemm_big_fits(epi, A, lda, M, N, K, ea)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_STORE: return launch_big<EPI_STORE>(A, lda, W, M, N, K, ea, st);
+    case EPI_RELU2: return launch_big<EPI_RELU2>(A, lda, W, M, N, K, ea, st);
+    case EPI_RESID_ATTN: return launch_big<EPI_RESID_ATTN>(A, lda, W, M, N, K, ea, st);
+    case EPI_RESID_MLP: return launch_big<EPI_RESID_MLP>(A, lda, W, M, N, K, ea, st);
+    case EPI_QKV: return launch_big<EPI_QKV>(A, lda, W, M, N, K, ea, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ann

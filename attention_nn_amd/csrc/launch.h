@@ -100,6 +100,15 @@ bool gemm_skinny_fits(int M, int N, int K, bool rms);
 bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea);
 // k_gemm over `batch` independent problems (blockIdx.z); epilogues STORE,
 // PE_B, PE_X; sOut / sX are the batch strides of ea.out / ea.x.
+// Large projections (prefill, training forward): 256 x 256 tiles, one work-
+// group per CU, AGPR accumulators, staged 16-byte epilogues.  Takes EPI_STORE,
+// EPI_RELU2, EPI_RESID_ATTN, EPI_RESID_MLP and EPI_QKV; gemm_big_fits says
+// whether a shape can go there, gemm_big_routes which epilogues gemm() sends
+// there by itself (those measured faster than the k_gemm_2w tiles).
+bool gemm_big_fits(int epi, const bf16_t* A, int lda, int M, int N, int K, const EpiArgs& ea);
+bool gemm_big_routes(int epi);
+hipError_t gemm_big(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
+                    const EpiArgs& ea, hipStream_t st);
 hipError_t gemm_batched(int epi, const bf16_t* A, int lda, long long sA, const bf16_t* W,
                         long long sW, int M, int N, int K, const EpiArgs& ea, long long sOut,
                         long long sX, int batch, hipStream_t st);

@@ -558,3 +558,56 @@ def test_sample_api_slides_window_like_reference():
         lg = R.logits(cfg, p, ctx)[0, -1]
         ids.append(int(np.argmax(lg.numpy())))
     assert got == ids[50:]
+
+
+# ---- the 256 x 256 prefill GEMM (gemm_big.hip) -------------------------------
+
+def _big_cfg(dh):
+    return GPTConfig(vocab_size=4096, num_layers=2, num_heads=768 // dh if dh == 128 else 8,
+                     model_dim=768 if dh == 128 else 512, seq_len=512, window=100,
+                     long_layers=(1,))
+
+
+@pytest.mark.parametrize("dh", [128, 64])
+def test_big_gemm_prefill_every_position(dh, monkeypatch):
+    """A prefill of 16 x 500 tokens (8000 rows: a ragged last 256-row tile)
+    puts the QKV (fused QK-norm / RoPE / cache epilogue), fc (relu^2) and, at
+    d = 768, the o / proj (residual mixes) projections on the 256 x 256 GEMM;
+    logits at every position against the oracle, and against the same
+    forward on the previous tiles (ANN_GEMM_BIG=0)."""
+    cfg = _big_cfg(dh)
+    p = perturb_lambdas(init_params(cfg, 71, dense=True))
+    tok = np.random.default_rng(72).integers(0, cfg.vocab_size, (16, 500))
+    print(f"case big gemm dh={dh} B=16 T=500", flush=True)
+    eng = _engine(cfg, p, 16)
+    monkeypatch.setenv("ANN_GEMM_BIG", "2")    # every epilogue the kernel takes
+    got = eng.forward_logits(tok).cpu()
+    monkeypatch.setenv("ANN_GEMM_BIG", "1")    # the routed ones (fc, o-proj)
+    routed = eng.forward_logits(tok).cpu()
+    monkeypatch.setenv("ANN_GEMM_BIG", "0")
+    old = eng.forward_logits(tok).cpu()
+    monkeypatch.delenv("ANN_GEMM_BIG")
+    # same products in the same k order: equal up to the order of the K tiles'
+    # accumulation inside an MFMA (measured bitwise equal)
+    assert (got - old).abs().max().item() < 2e-3
+    assert (routed - old).abs().max().item() < 2e-3
+    ref = R.logits(cfg, p, tok)
+    err = max((got - ref).abs().max().item(), (routed - ref).abs().max().item())
+    assert err < LOGIT_TOL, err
+
+
+def test_big_gemm_training_forward():
+    """GPT.__call__ on 16 x 500 tokens (the body's projections on the 256 x
+    256 GEMM, the lm_head's CE epilogue on the previous tiles): per-row losses
+    against the oracle."""
+    cfg = _big_cfg(128)
+    p = perturb_lambdas(init_params(cfg, 73, dense=True))
+    rng = np.random.default_rng(74)
+    tok = rng.integers(0, cfg.vocab_size, (16, 500))
+    tgt = rng.integers(0, cfg.vocab_size, (16, 500))
+    print("case big gemm training forward", flush=True)
+    eng = _engine(cfg, p, 16)
+    mean, rows = eng.forward_loss(tok, tgt, rows=True)
+    rm, rr = R.loss(cfg, p, tok, tgt, banded_bf16=True)
+    assert (rows.cpu().double() - rr.double()).abs().max().item() < 1e-2
+    assert abs(mean.item() - rm.item()) < 5e-4
