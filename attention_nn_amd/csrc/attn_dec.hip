@@ -277,25 +277,30 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     __hip_atomic_fetch_add(cnt + b * H + h, 64u - (unsigned)nsplit, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   if (tid < DH) {
-    // up to 8 splits' words loaded at once; a word not yet carrying the tag
-    // is waited for (split order of the sums unchanged)
+    // up to 8 splits' words loaded at once; the words not yet carrying the
+    // tag are re-read together (split order of the sums unchanged)
     float o = 0.f, l = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      const u64* po[8];
+      const u64* pl[8];
       u64 vo[8], vl[8];
+      bool ok[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const u64* w = pbase + (size_t)min(s0 + j, nsplit - 1) * (DH + 1);
-        vo[j] = ll_load(w + tid);
-        vl[j] = ll_load(w + DH);
+        ok[j] = s0 + j < nsplit;
+        po[j] = w + tid;
+        pl[j] = w + DH;
+        vo[j] = ll_load(po[j]);
+        vl[j] = ll_load(pl[j]);
       }
+      ll_settle<8>(po, vo, ok, tag, err);
+      ll_settle<8>(pl, vl, ok, tag, err);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if (s0 + j >= nsplit) break;
-        const u64* w = pbase + (size_t)(s0 + j) * (DH + 1);
-        o += __uint_as_float((uint32_t)(vo[j] >> 32) == tag ? (uint32_t)vo[j]
-                                                             : ll_wait(w + tid, tag, err));
-        l += __uint_as_float((uint32_t)(vl[j] >> 32) == tag ? (uint32_t)vl[j]
-                                                             : ll_wait(w + DH, tag, err));
+        if (!ok[j]) break;
+        o += __uint_as_float((uint32_t)vo[j]);
+        l += __uint_as_float((uint32_t)vl[j]);
       }
     }
     out[(size_t)b * d + h * DH + tid] = f2bf(o / l);

@@ -122,24 +122,50 @@ __device__ __forceinline__ void ll_store(u64* p, uint32_t v, uint32_t tag) {
 __device__ __forceinline__ u64 ll_load(const u64* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The waits below are inlined at every use: an out-of-line call opens with a
+// wait for all of the caller's outstanding loads (prefetched weights, K/V
+// rows), and through a generic pointer every poll becomes a flat load whose
+// wait also covers LDS traffic.  Inline, the polls are global loads and the
+// compiler waits for exactly the loads it needs.
+//
 // Wait until the word carries `tag` and return its data.  Bounded: after
-// LL_SPIN polls, or at once when another wait has already given up (*err set),
-// it sets *err and returns whatever it read.  Two polls stay in flight, so a
-// ready word is seen about one load latency after it lands instead of up to
-// two; no sleep between them (measured faster).
-__device__ __noinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
-  u64 a = ll_load(p);
-  for (unsigned s = 0;; s += 2) {
-    const u64 b = ll_load(p);
-    if ((uint32_t)(a >> 32) == tag) return (uint32_t)a;
-    if ((s & 127u) == 0 && s) {
+// LL_SPIN polls, or once another wait has already given up (*err set), it
+// sets *err and returns whatever it read last.
+__device__ __forceinline__ uint32_t ll_wait(const u64* p, uint32_t tag, unsigned* err) {
+  u64 v = ll_load(p);
+  for (unsigned s = 1; (uint32_t)(v >> 32) != tag; ++s) {
+    if ((s & 63u) == 0) {
       if (s >= LL_SPIN) {
         atomicOr(err, 1u);
-        return (uint32_t)b;
+        break;
       }
-      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return (uint32_t)b;
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
     }
-    a = ll_load(p);
-    if ((uint32_t)(b >> 32) == tag) return (uint32_t)b;
+    v = ll_load(p);
+  }
+  return (uint32_t)v;
+}
+// N words at once: v[j] holds a value already read from p[j] (ok[j] false:
+// not a word of this thread, never waited for).  Re-reads the words that do
+// not carry `tag` yet, all of them together, until every one does; bounded
+// like ll_wait.
+template <int N>
+__device__ __forceinline__ void ll_settle(const u64* const (&p)[N], u64 (&v)[N], const bool (&ok)[N],
+                                          uint32_t tag, unsigned* err) {
+  for (unsigned s = 1;; ++s) {
+    bool done = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) done = done && (!ok[j] || (uint32_t)(v[j] >> 32) == tag);
+    if (done) return;
+    if ((s & 63u) == 0) {
+      if (s >= LL_SPIN) {
+        atomicOr(err, 1u);
+        return;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (ok[j] && (uint32_t)(v[j] >> 32) != tag) v[j] = ll_load(p[j]);
   }
 }

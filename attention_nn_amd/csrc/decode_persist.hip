@@ -20,6 +20,7 @@
 //   2  attention of (head h, split s): QK-norm, RoPE, cache append, softmax
 //      partial (O, L) with a fixed shift (|s| <= scale Dh) -> xp
 //   3  o = sum_s O_s / sum_s L_s; x' = mix_attn(x, x0, o Wo^T)  -> xm
+//      (rows on the work-groups that ran no attention in phase 2)
 //   4  h = relu2(rms(x') Wfc^T)                   -> xh
 //   5  x = mix_mlp(x', h Wproj^T)                 -> xx
 // then z = rms(x) lm_head^T: greedy keys (bf16 order << 16 | 0xffff - n) per
@@ -56,20 +57,28 @@ __device__ __forceinline__ float pd_dot8(const uint4& w, const uint4& x, float c
   return pd_dot2(w.w, x.w, c);
 }
 
-// dst[i] = data of src[i] for i < n, all loads of a thread issued first.
+// dst[i] = data of src[i] for i < n (n >= 1): up to 8 words per thread read
+// at once, then the ones not yet tagged re-read together.  Slots past n load
+// nothing (a clamped address would have every work-group poll the last word
+// up to 7 more times per thread, measured slower).
 __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, uint32_t tag,
                                         unsigned* err) {
   for (int i0 = 0; i0 < n; i0 += PD_T * 8) {
+    const u64* p[8];
     u64 v[8];
+    bool ok[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = i0 + j * PD_T + (int)threadIdx.x;
-      v[j] = i < n ? ll_load(src + i) : 0ull;
+      ok[j] = i < n;
+      p[j] = src + min(i, n - 1);
+      v[j] = ok[j] ? ll_load(p[j]) : 0ull;
     }
+    ll_settle<8>(p, v, ok, tag, err);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = i0 + j * PD_T + (int)threadIdx.x;
-      if (i < n) dst[i] = (uint32_t)(v[j] >> 32) == tag ? (uint32_t)v[j] : ll_wait(src + i, tag, err);
+      if (ok[j]) dst[i] = (uint32_t)v[j];
     }
   }
 }
@@ -79,9 +88,14 @@ __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, ui
 // d > 512: the 155M step fits 128-192 work-groups (neutral at 256, measured).
 constexpr int pd_rows_per_wave(int ud) { return ud >= 2 ? 3 : 2; }
 
-// Rows of a projection owned by work-group g: pairs [b, e) of npairs.
-__device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr) {
-  const int g = blockIdx.x, G = gridDim.x;
+// Rows of a projection owned by work-group g: pairs [b, e) of npairs, split
+// over the work-groups from `first` on (none for the ones before it).
+__device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr, int first = 0) {
+  const int g = (int)blockIdx.x - first, G = (int)gridDim.x - first;
+  if (g < 0) {
+    n0 = nr = 0;
+    return;
+  }
   const int b = (int)((long long)npairs * g / G), e = (int)((long long)npairs * (g + 1) / G);
   n0 = 2 * b;
   nr = 2 * (e - b);
@@ -175,14 +189,16 @@ __device__ __forceinline__ void pd_rms(const bf16_t* src, bf16_t* dst, int K, fl
 enum { PE_STORE = 0, PE_ATTN = 1, PE_RELU2 = 2, PE_MLP = 3 };
 
 // Epilogue of this work-group's rows [n0, n0 + nr) and tagged stores of the
-// bf16 pairs to dst (row stride rw words).
+// bf16 pairs to dst (row stride rw words), to each of `rep` copies cst words
+// apart.
 template <int E, int BM>
 __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr, u64* dst, int rw,
                                         uint32_t tag, const float* lam, const bf16_t* xr,
-                                        const bf16_t* x0, int d) {
-  const int np = nr >> 1;
-  for (int i = threadIdx.x; i < BM * np; i += PD_T) {
-    const int b = i / np, j = i - b * np, n = n0 + 2 * j;
+                                        const bf16_t* x0, int d, int rep = 1, int cst = 0) {
+  const int np = nr >> 1, tot = BM * np;
+  for (int i = threadIdx.x; i < rep * tot; i += PD_T) {
+    const int cp = i / tot, k = i - cp * tot;
+    const int b = k / np, j = k - b * np, n = n0 + 2 * j;
     const float y0 = stage[b][2 * j], y1 = stage[b][2 * j + 1];
     uint32_t v;
     if (E == PE_STORE) {
@@ -198,7 +214,7 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
       const bf16_t c = mix_mlp(lam, bf2f(xr[b * d + n + 1]), y1);
       v = (uint32_t)a | ((uint32_t)c << 16);
     }
-    ll_store(dst + (size_t)b * rw + (n >> 1), v, tag);
+    ll_store(dst + (size_t)cp * cst + (size_t)b * rw + (n >> 1), v, tag);
   }
 }
 
@@ -225,6 +241,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = gridDim.x, g = blockIdx.x;
   const int d = P.d, H = P.H, d2 = d >> 1;
+  // this work-group's copy of the x' / x exchange (spreads the pollers of
+  // each word over rep copies)
+  const u64* xm_me = P.xm + (size_t)(g % P.rep) * P.rep_stride;
+  const u64* xx_me = P.xx + (size_t)(g % P.rep) * P.rep_stride;
   bf16_t* sx0 = (bf16_t*)lds4;        // x0 (BM x d)
   bf16_t* sxs = sx0 + BM * d;         // layer input x
   bf16_t* sxm = sxs + BM * d;         // x after attention
@@ -233,6 +253,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
   const uint32_t tb = __hip_atomic_load(P.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * PD_PH;
   if (tid < BM) s_pos[tid] = P.pos[tid];
+
+  // layer 0's qkv weights first: their loads do not depend on the token
+  uint4 wr[PD_SLOTS];
+  {
+    int n0, nr;
+    pd_rows(3 * d2, n0, nr);
+    pd_wload<UD, RD>(P.layers + P.o_qkv, d, n0, nr, wr);
+  }
 
   // ---- x = x0 = rms(embed[tok]) (every work-group, redundantly)
   for (int b = 0; b < BM; ++b) {
@@ -246,7 +274,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   for (int i = tid; i < BM * d2; i += PD_T) ((uint32_t*)sxs)[i] = ((const uint32_t*)sx0)[i];
   __syncthreads();
 
-  uint4 wr[PD_SLOTS];
   for (int l = 0; l < P.L; ++l) {
     const bf16_t* Wl = P.layers + P.lstride * l;
     const float* lam = P.lam + 8 * l;
@@ -256,9 +283,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
     // ---- 1: qkv
     pd_rows(3 * d2, n0, nr);
-    pd_wload<UD, RD>(Wl + P.o_qkv, d, n0, nr, wr);
+    if (l > 0) pd_wload<UD, RD>(Wl + P.o_qkv, d, n0, nr, wr);
     if (l > 0) {
-      ll_poll(P.xx, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
+      ll_poll(xx_me, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
       __syncthreads();
     }
     pd_rms<BM>(sxs, gin, d, P.eps, red);
@@ -266,11 +293,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     pd_emit<PE_STORE, BM>(stage, n0, nr, P.xq, 3 * d2, t1, lam, nullptr, nullptr, d);
 
     // ---- 2: attention of (b, h, split)
-    pd_rows(d2, n0, nr);
     const int S = lng ? P.s_long : P.s_win;
-    const bool attn = g < BM * H * S;
-    // o projection weights for phase 3: now on work-groups without attention,
-    // after it on the others (keeps the K/V ring and these apart)
+    const int NA = BM * H * S;   // work-groups 0 .. NA-1 run the attention
+    const bool attn = g < NA;
+    // phase 3 (o projection) runs on the other work-groups, whose weights
+    // load during the attention; the attention work-groups go on to phase 4
+    pd_rows(d2, n0, nr, NA);
     if (!attn) pd_wload<UD, RD>(Wl + P.o_o, d, n0, nr, wr);
     if (attn) {
       const int s = g % S, h = (g / S) % H, b = g / (S * H);
@@ -427,11 +455,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         for (int w = 0; w < PD_NW; ++w) lt += s_l[w];
         ll_store(dst + DH, __float_as_uint(lt), t1 + 1u);
       }
-      pd_wload<UD, RD>(Wl + P.o_o, d, n0, nr, wr);
     }
 
     // ---- 3: o = combine(partials); x' = mix_attn(x, x0, o Wo^T)
-    {
+    if (!attn) {
       const int nw = BM * H * S * (DH + 1);
       ll_poll(P.xp, nw, (uint32_t*)spart, t1 + 1u, P.err);
       __syncthreads();
@@ -447,13 +474,13 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       }
       __syncthreads();
       pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
-      pd_emit<PE_ATTN, BM>(stage, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d);
+      pd_emit<PE_ATTN, BM>(stage, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d, P.rep, P.rep_stride);
     }
 
     // ---- 4: h = relu2(rms(x') Wfc^T)
     pd_rows(2 * d, n0, nr);
     pd_wload<UD, RD>(Wl + P.o_fc, d, n0, nr, wr);
-    ll_poll(P.xm, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
+    ll_poll(xm_me, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
     __syncthreads();
     pd_rms<BM>(sxm, gin, d, P.eps, red);
     pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
@@ -465,7 +492,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     ll_poll(P.xh, BM * 2 * d, (uint32_t*)gin, t1 + 3u, P.err);
     __syncthreads();
     pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)gin, 4 * d, nr, stage);
-    pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d);
+    pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d, P.rep, P.rep_stride);
   }
 
   // ---- lm_head over this work-group's rows [r0, r1), two register batches
@@ -529,7 +556,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   uint4 wa[PD_SLOTS], wb[PD_SLOTS];
   const int nbe = (nb + 1) & ~1;
   if (nb > 0) hload(0, wa);
-  ll_poll(P.xx, BM * d2, (uint32_t*)sxs, tl, P.err);
+  ll_poll(xx_me, BM * d2, (uint32_t*)sxs, tl, P.err);
   __syncthreads();
   pd_rms<BM>(sxs, gin, d, P.eps, red);
   for (int k = 0; k < nbe; k += 2) {
@@ -600,8 +627,10 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
     return false;
   const int d2 = d / 2, rd = PD_NW * pd_rows_per_wave(ud);
   auto rows = [&](int npairs) { return 2 * ((npairs + G - 1) / G); };
-  if (rows(3 * d2) > rd || rows(d2) > rd || rows(2 * d) > rd || rows(d2) > PD_NW) return false;
-  if (B * H * s_long > G || s_long < 1) return false;
+  if (rows(3 * d2) > rd || rows(2 * d) > rd || rows(d2) > PD_NW) return false;
+  // o projection over the work-groups without attention (fewest at the long layers)
+  const int na = B * H * s_long;
+  if (na >= G || s_long < 1 || 2 * ((d2 + (G - na) - 1) / (G - na)) > rd) return false;
   return true;
 }
 

@@ -79,15 +79,17 @@ struct SLayout {  // byte offsets into the workspace
 };
 
 // Exchange area of the persistent decode step (batch 1): tagged words of
-// xq, xp, xm, xh, xx, xk, then the generation and error words.  With
-// `which` = 1..8 returns the byte offset of that part, 0 the total size.
+// xq, xp, xm, xh, xx, xk, then the generation and error words; xm and xx
+// hold PD_MAX_REP copies pd_rep_stride words apart.  With `which` = 1..8
+// returns the byte offset of that part, 0 the total size.
 constexpr int PD_BATCH = 1;
 constexpr int PD_MAX_SLONG = 8;
 constexpr int PD_MAX_G = 1024;
+size_t pd_rep_stride(const ann_config& c) { return ((size_t)PD_BATCH * c.d / 2 + 63) / 64 * 64; }
 size_t pd_layout(const ann_config& c, int which) {
-  const size_t d = c.d, H = c.H, Dh = d / c.H, B = PD_BATCH;
-  const size_t parts[8] = {B * 3 * d / 2, B * H * PD_MAX_SLONG * (Dh + 1), B * d / 2, B * 2 * d,
-                           B * d / 2, (size_t)PD_MAX_G * B, 1, 1};
+  const size_t d = c.d, H = c.H, Dh = d / c.H, B = PD_BATCH, rs = pd_rep_stride(c);
+  const size_t parts[8] = {B * 3 * d / 2, B * H * PD_MAX_SLONG * (Dh + 1), PD_MAX_REP * rs, B * 2 * d,
+                           PD_MAX_REP * rs, (size_t)PD_MAX_G * B, 1, 1};
   size_t off = 0;
   for (int i = 0; i < 8; ++i) {
     if (which == i + 1) return off;
@@ -206,6 +208,7 @@ struct ann_ctx {
   // decode attention: splits per (row, head) fixed by ANN_DEC_SPLITS (0: sized
   // by the batch, about 384 work-groups)
   int dec_split_env = 0;
+  int pd_rep = PD_MAX_REP;   // copies of the persistent step's x' / x exchange
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -589,6 +592,8 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.s_win = pd_splits(c, B, false);
   P.s_long = pd_splits(c, B, true);
   P.greedy = greedy ? 1 : 0;
+  P.rep = c->pd_rep;
+  P.rep_stride = (int)pd_rep_stride(g);
   P.scale = g.attn_scale;
   P.shift = g.attn_scale * (float)c->Dh * 1.02f;
   P.eps = g.rms_eps;
@@ -658,6 +663,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->use_graph = !(ge && ge[0] == '0');
   const char* pe = getenv("ANN_PERSIST");
   c->pd_env = !(pe && pe[0] == '0');
+  const char* pr = getenv("ANN_PD_REP");
+  if (pr && atoi(pr) >= 1 && atoi(pr) <= PD_MAX_REP) c->pd_rep = atoi(pr);
   const char* ds = getenv("ANN_DEC_SPLITS");
   c->dec_split_env = ds ? atoi(ds) : 0;
   if (c->dec_split_env < 0 || c->dec_split_env > MAX_SPLIT) c->dec_split_env = 0;

@@ -210,15 +210,17 @@ struct PDParams {
   float* logits;          // optional fp32 softcapped logits (B, V)
   u64* xq;                // qkv       B x 3d/2 words
   u64* xp;                // partials  B*H*s_long x (Dh+1)
-  u64* xm;                // x'        B x d/2
+  u64* xm;                // x'        rep copies of B x d/2, rep_stride words apart
   u64* xh;                // hidden    B x 2d
-  u64* xx;                // x         B x d/2
+  u64* xx;                // x         rep copies of B x d/2, rep_stride words apart
   u64* xk;                // keys      G x B
   unsigned* gen;          // step generation (tags)
   unsigned* err;          // set when a bounded wait timed out
   int d, H, L, V, Vs, max_ctx, window, s_win, s_long, greedy;
+  int rep, rep_stride;    // copies of xm / xx (1..PD_MAX_REP); work-group g reads copy g % rep
   float scale, shift, eps;
 };
+constexpr int PD_MAX_REP = 8;
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
 hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st);
