@@ -209,6 +209,7 @@ struct ann_ctx {
   // by the batch, about 384 work-groups)
   int dec_split_env = 0;
   int pd_rep = PD_MAX_REP;   // copies of the persistent step's x' / x exchange
+  int pd_on = 0;             // work-groups for the o rows (0: d / 8, 8 rows each)
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -593,6 +594,7 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.s_long = pd_splits(c, B, true);
   P.greedy = greedy ? 1 : 0;
   P.rep = c->pd_rep;
+  P.on = c->pd_on > 0 ? c->pd_on : g.d / 8;
   P.rep_stride = (int)pd_rep_stride(g);
   P.scale = g.attn_scale;
   P.shift = g.attn_scale * (float)c->Dh * 1.02f;
@@ -663,6 +665,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->use_graph = !(ge && ge[0] == '0');
   const char* pe = getenv("ANN_PERSIST");
   c->pd_env = !(pe && pe[0] == '0');
+  const char* on = getenv("ANN_PD_ON");
+  c->pd_on = on && atoi(on) > 0 ? atoi(on) : 0;
   const char* pr = getenv("ANN_PD_REP");
   if (pr && atoi(pr) >= 1 && atoi(pr) <= PD_MAX_REP) c->pd_rep = atoi(pr);
   const char* ds = getenv("ANN_DEC_SPLITS");

@@ -218,6 +218,7 @@ struct PDParams {
   unsigned* err;          // set when a bounded wait timed out
   int d, H, L, V, Vs, max_ctx, window, s_win, s_long, greedy;
   int rep, rep_stride;    // copies of xm / xx (1..PD_MAX_REP); work-group g reads copy g % rep
+  int on;                 // work-groups holding the o rows (at most, after the attention ones)
   float scale, shift, eps;
 };
 constexpr int PD_MAX_REP = 8;
