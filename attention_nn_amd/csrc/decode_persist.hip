@@ -83,10 +83,11 @@ __device__ __forceinline__ void ll_poll(const u64* src, int n, uint32_t* dst, ui
   }
 }
 
-// Rows per wave of the K = d projections held in registers (U = UD chunks
-// each); the K = 4d projection holds one row of 4 UD chunks.  Three for
-// d > 512: the 155M step fits 128-192 work-groups (neutral at 256, measured).
-constexpr int pd_rows_per_wave(int ud) { return ud >= 2 ? 3 : 2; }
+// The K = d projections (qkv, o, fc) give each wave up to PD_PW pairs of
+// consecutive rows (PD_PW * 2 * UD weight chunks per lane in registers), so
+// a wave forms its own bf16 pairs and stores them without LDS staging or a
+// barrier; the K = 4d projection holds one row of 4 UD chunks per wave.
+constexpr int PD_PW = 2;
 
 // Rows of a projection owned by work-group g: pairs [b, e) of npairs, split
 // over the `count` work-groups from `first` on (none for the others).
@@ -188,6 +189,82 @@ __device__ __forceinline__ void pd_rms(const bf16_t* src, bf16_t* dst, int K, fl
 
 enum { PE_STORE = 0, PE_ATTN = 1, PE_RELU2 = 2, PE_MLP = 3 };
 
+// Epilogue of outputs n, n + 1 of row b: the bf16 pair of one tagged word.
+template <int E>
+__device__ __forceinline__ uint32_t pd_epi(float y0, float y1, int b, int n, const float* lam,
+                                           const bf16_t* xr, const bf16_t* x0, int d) {
+  if (E == PE_STORE) return pack2(y0, y1);
+  if (E == PE_RELU2) return (uint32_t)relu2_bf(y0) | ((uint32_t)relu2_bf(y1) << 16);
+  if (E == PE_ATTN) {
+    const bf16_t a = mix_attn(lam, bf2f(xr[b * d + n]), bf2f(x0[b * d + n]), y0);
+    const bf16_t c = mix_attn(lam, bf2f(xr[b * d + n + 1]), bf2f(x0[b * d + n + 1]), y1);
+    return (uint32_t)a | ((uint32_t)c << 16);
+  }
+  const bf16_t a = mix_mlp(lam, bf2f(xr[b * d + n]), y0);
+  const bf16_t c = mix_mlp(lam, bf2f(xr[b * d + n + 1]), y1);
+  return (uint32_t)a | ((uint32_t)c << 16);
+}
+
+// Weight chunks of this lane for the pair path: pairs q = wave + NW k
+// (k < PD_PW), rows 2q and 2q + 1 of [n0, n0 + nr), chunks lane + 64 u.
+template <int U>
+__device__ __forceinline__ void pd_wload2(const bf16_t* W, int K, int n0, int nr, uint4* wr) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
+#pragma unroll
+  for (int k = 0; k < PD_PW; ++k) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = 2 * (wv + PD_NW * k) + h;
+      const bool ok = r < nr;
+      const uint4* row = (const uint4*)(W + (size_t)(n0 + (ok ? r : 0)) * K);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = lane + 64 * u;
+        wr[(2 * k + h) * U + u] = (ok && c < K8) ? row[c] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+}
+
+// Dots of this wave's pairs with gin, epilogue, and the tagged stores of the
+// pairs to dst (row stride rw words) and its rep copies cst words apart --
+// per wave, as soon as its own sums are done.
+template <int E, int U, int BM>
+__device__ __forceinline__ void pd_wdot2(const uint4* wr, const uint4* gin, int K, int n0, int nr,
+                                         u64* dst, int rw, uint32_t tag, const float* lam,
+                                         const bf16_t* xr, const bf16_t* x0, int d, int rep,
+                                         int cst) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, K8 = K >> 3;
+#pragma unroll
+  for (int k = 0; k < PD_PW; ++k) {
+    const int q = wv + PD_NW * k;
+    if (2 * q < nr) {
+      float a0[BM], a1[BM];
+#pragma unroll
+      for (int b = 0; b < BM; ++b) a0[b] = a1[b] = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = lane + 64 * u;
+        if (c < K8) {
+#pragma unroll
+          for (int b = 0; b < BM; ++b) {
+            a0[b] = pd_dot8(wr[(2 * k) * U + u], gin[b * K8 + c], a0[b]);
+            a1[b] = pd_dot8(wr[(2 * k + 1) * U + u], gin[b * K8 + c], a1[b]);
+          }
+        }
+      }
+      const int n = n0 + 2 * q;
+#pragma unroll
+      for (int b = 0; b < BM; ++b) {
+        const float y0 = wave_sum(a0[b]), y1 = wave_sum(a1[b]);   // in every lane
+        if (lane < rep)
+          ll_store(dst + (size_t)lane * cst + (size_t)b * rw + (n >> 1),
+                   pd_epi<E>(y0, y1, b, n, lam, xr, x0, d), tag);
+      }
+    }
+  }
+}
+
 // Epilogue of this work-group's rows [n0, n0 + nr) and tagged stores of the
 // bf16 pairs to dst (row stride rw words), to each of `rep` copies cst words
 // apart.
@@ -199,21 +276,7 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
   for (int i = threadIdx.x; i < rep * tot; i += PD_T) {
     const int cp = i / tot, k = i - cp * tot;
     const int b = k / np, j = k - b * np, n = n0 + 2 * j;
-    const float y0 = stage[b][2 * j], y1 = stage[b][2 * j + 1];
-    uint32_t v;
-    if (E == PE_STORE) {
-      v = pack2(y0, y1);
-    } else if (E == PE_RELU2) {
-      v = (uint32_t)relu2_bf(y0) | ((uint32_t)relu2_bf(y1) << 16);
-    } else if (E == PE_ATTN) {
-      const bf16_t a = mix_attn(lam, bf2f(xr[b * d + n]), bf2f(x0[b * d + n]), y0);
-      const bf16_t c = mix_attn(lam, bf2f(xr[b * d + n + 1]), bf2f(x0[b * d + n + 1]), y1);
-      v = (uint32_t)a | ((uint32_t)c << 16);
-    } else {
-      const bf16_t a = mix_mlp(lam, bf2f(xr[b * d + n]), y0);
-      const bf16_t c = mix_mlp(lam, bf2f(xr[b * d + n + 1]), y1);
-      v = (uint32_t)a | ((uint32_t)c << 16);
-    }
+    const uint32_t v = pd_epi<E>(stage[b][2 * j], stage[b][2 * j + 1], b, n, lam, xr, x0, d);
     ll_store(dst + (size_t)cp * cst + (size_t)b * rw + (n >> 1), v, tag);
   }
 }
@@ -224,7 +287,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int VD = DH / 64;       // output dims per lane in P.V
   constexpr int P2 = DH / 2, D4 = DH / 4;
   constexpr int PD_RING = DH == 128 ? 2 : 3;   // key chunks in flight per wave
-  constexpr int RD = pd_rows_per_wave(UD);      // rows per wave, K = d projections
 
   extern __shared__ uint4 lds4[];
   __shared__ float stage[BM][PD_RMAX];
@@ -248,8 +310,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   bf16_t* sx0 = (bf16_t*)lds4;        // x0 (BM x d)
   bf16_t* sxs = sx0 + BM * d;         // layer input x
   bf16_t* sxm = sxs + BM * d;         // x after attention
-  bf16_t* gin = sxm + BM * d;         // projection input (BM x 4d)
-  float* spart = (float*)(gin + BM * 4 * d);   // attention partials
+  bf16_t* gin = sxm + BM * d;         // projection input (BM x d)
+  bf16_t* ghb = gin + BM * d;         // proj input h (BM x 4d): its own buffer, since
+                                      // waves poll it while others may still read gin
+  float* spart = (float*)(ghb + BM * 4 * d);   // attention partials
 
   const uint32_t tb = __hip_atomic_load(P.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * PD_PH;
   if (tid < BM) s_pos[tid] = P.pos[tid];
@@ -259,7 +323,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   {
     int n0, nr;
     pd_rows(3 * d2, n0, nr, 0, G);
-    pd_wload<UD, RD>(P.layers + P.o_qkv, d, n0, nr, wr);
+    pd_wload2<UD>(P.layers + P.o_qkv, d, n0, nr, wr);
   }
 
   // ---- x = x0 = rms(embed[tok]) (every work-group, redundantly)
@@ -283,14 +347,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
     // ---- 1: qkv
     pd_rows(3 * d2, n0, nr, 0, G);
-    if (l > 0) pd_wload<UD, RD>(Wl + P.o_qkv, d, n0, nr, wr);
+    if (l > 0) pd_wload2<UD>(Wl + P.o_qkv, d, n0, nr, wr);
     if (l > 0) {
       ll_poll(xx_me, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
       __syncthreads();
     }
     pd_rms<BM>(sxs, gin, d, P.eps, red);
-    pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
-    pd_emit<PE_STORE, BM>(stage, n0, nr, P.xq, 3 * d2, t1, lam, nullptr, nullptr, d);
+    pd_wdot2<PE_STORE, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xq, 3 * d2, t1, lam, nullptr,
+                               nullptr, d, 1, 0);
 
     // ---- 2: attention of (b, h, split)
     const int S = lng ? P.s_long : P.s_win;
@@ -301,7 +365,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     // on to phase 4 (fewer producers of x' exchange faster: 8 rows each on
     // 96 work-groups measured 1.5% faster per step than 4-6 on 144-174)
     pd_rows(d2, n0, nr, NA, min(P.on, G - NA));
-    if (!attn) pd_wload<UD, RD>(Wl + P.o_o, d, n0, nr, wr);
+    if (!attn) pd_wload2<UD>(Wl + P.o_o, d, n0, nr, wr);
     if (attn) {
       const int s = g % S, h = (g / S) % H, b = g / (S * H);
       const int p = s_pos[b];
@@ -475,25 +539,25 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         gin[i] = f2bf(o / lt);
       }
       __syncthreads();
-      pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
-      pd_emit<PE_ATTN, BM>(stage, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d, P.rep, P.rep_stride);
+      pd_wdot2<PE_ATTN, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d,
+                                P.rep, P.rep_stride);
     }
 
     // ---- 4: h = relu2(rms(x') Wfc^T)
     pd_rows(2 * d, n0, nr, 0, G);
-    pd_wload<UD, RD>(Wl + P.o_fc, d, n0, nr, wr);
+    pd_wload2<UD>(Wl + P.o_fc, d, n0, nr, wr);
     ll_poll(xm_me, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
     __syncthreads();
     pd_rms<BM>(sxm, gin, d, P.eps, red);
-    pd_wdot<UD, RD, BM>(wr, (const uint4*)gin, d, nr, stage);
-    pd_emit<PE_RELU2, BM>(stage, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr, nullptr, d);
+    pd_wdot2<PE_RELU2, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr,
+                               nullptr, d, 1, 0);
 
     // ---- 5: x = mix_mlp(x', h Wproj^T)
     pd_rows(d2, n0, nr, 0, G);
     pd_wload<4 * UD, 1>(Wl + P.o_proj, 4 * d, n0, nr, wr);
-    ll_poll(P.xh, BM * 2 * d, (uint32_t*)gin, t1 + 3u, P.err);
+    ll_poll(P.xh, BM * 2 * d, (uint32_t*)ghb, t1 + 3u, P.err);
     __syncthreads();
-    pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)gin, 4 * d, nr, stage);
+    pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)ghb, 4 * d, nr, stage);
     pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d, P.rep, P.rep_stride);
   }
 
@@ -627,7 +691,7 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
   if (B != 1 || ud == 0 || (Dh != 64 && Dh != 128) || d % 16 || V % 2 || V > 65536 || L > 50 ||
       G < 1)
     return false;
-  const int d2 = d / 2, rd = PD_NW * pd_rows_per_wave(ud);
+  const int d2 = d / 2, rd = 2 * PD_PW * PD_NW;
   auto rows = [&](int npairs) { return 2 * ((npairs + G - 1) / G); };
   if (rows(3 * d2) > rd || rows(2 * d) > rd || rows(d2) > PD_NW) return false;
   // o projection over the work-groups without attention (fewest at the long layers)
@@ -637,7 +701,7 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
 }
 
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
-  return (size_t)7 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
+  return (size_t)8 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
 }
 
 // Launch of the G work-groups.  G is at most the CU count and a CU holds one
@@ -670,7 +734,7 @@ hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hi
   const size_t lds = decode_persist_lds(B, P.d, P.H, Dh, P.s_long);
   if (lds > 144 * 1024 || B != 1) return hipErrorInvalidValue;
   // o rows per work-group within what its registers hold
-  const int ud = decode_persist_slots(P.d), rd = PD_NW * pd_rows_per_wave(ud);
+  const int rd = 2 * PD_PW * PD_NW;
   const int no = P.on < G - B * P.H * P.s_long ? P.on : G - B * P.H * P.s_long;
   if (no < 1 || 2 * ((P.d / 2 + no - 1) / no) > rd) return hipErrorInvalidValue;
   switch (Dh * 16 + decode_persist_slots(P.d)) {
