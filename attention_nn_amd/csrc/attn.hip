@@ -47,7 +47,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
   __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KP];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[BK * KP];
 
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // XCD-aware order: work-group L runs on XCD L % 8, so work item
+  // (L % 8) * N/8 + L / 8 puts consecutive items -- the query blocks of one
+  // (row, head), which read the same keys and values -- on one XCD and its L2
+  int qb, h, b;
+  {
+    const int nx = gridDim.x, ny = gridDim.y, N = nx * ny * gridDim.z;
+    const int L = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const int w = (N % 8 == 0) ? (L % 8) * (N / 8) + L / 8 : L;
+    qb = w % nx;
+    h = (w / nx) % ny;
+    b = w / (nx * ny);
+  }
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int d = H * DH;
