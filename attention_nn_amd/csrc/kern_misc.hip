@@ -131,6 +131,51 @@ __global__ __launch_bounds__(256) void k_rms_apply(const bf16_t* __restrict__ x,
   }
 }
 
+// The same with one wave per row (CPL 16-byte chunks per lane, d <= 512 CPL)
+// and four rows per work-group: the row sum is a wave reduction, no barrier.
+// One work-group per row left 160 of 256 threads idle at d = 768 and made
+// every row pay a barrier: 26.8 us for 32768 rows, a 100 MB round trip.
+template <int CPL>
+__global__ __launch_bounds__(256) void k_rms_rows(const bf16_t* __restrict__ x, int ldx,
+                                                  bf16_t* __restrict__ h, int ldh, int M, int d,
+                                                  float eps) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const uint4* r = (const uint4*)(x + (size_t)m * ldx);
+  uint4* o = (uint4*)(h + (size_t)m * ldh);
+  const int K8 = d >> 3;
+  uint4 v[CPL];
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) {
+    const int c = lane + u * 64;
+    v[u] = c < K8 ? r[c] : make_uint4(0, 0, 0, 0);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) {
+    float f[8];
+    unpack8(v[u], f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  }
+  const float s = rsqrtf(wave_sum(ss) / (float)d + eps);
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) {
+    const int c = lane + u * 64;
+    if (c < K8) {
+      float f[8];
+      unpack8(v[u], f);
+      uint4 w;
+      w.x = pack2(f[0] * s, f[1] * s);
+      w.y = pack2(f[2] * s, f[3] * s);
+      w.z = pack2(f[4] * s, f[5] * s);
+      w.w = pack2(f[6] * s, f[7] * s);
+      o[c] = w;
+    }
+  }
+}
+
 // ---- QK-norm + RoPE + KV-cache append --------------------------------------
 
 // qkv (M, 3*H*Dh) bf16 -> q (M, H*Dh) = rope(rms(q)); K/V cache rows written
@@ -337,7 +382,13 @@ hipError_t embed_rms(const int32_t* tok, const bf16_t* emb, bf16_t* x, bf16_t* x
 hipError_t rms_apply(const bf16_t* x, int ldx, bf16_t* h, int ldh, int M, int d, float eps,
                      hipStream_t st) {
   if (d > 8192 || d % 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rms_apply, dim3(M), dim3(256), 0, st, x, ldx, h, ldh, d, eps);
+  const dim3 g4(cdiv(M, 4));
+  if (d <= 1024)
+    hipLaunchKernelGGL(k_rms_rows<2>, g4, dim3(256), 0, st, x, ldx, h, ldh, M, d, eps);
+  else if (d <= 2048)
+    hipLaunchKernelGGL(k_rms_rows<4>, g4, dim3(256), 0, st, x, ldx, h, ldh, M, d, eps);
+  else
+    hipLaunchKernelGGL(k_rms_apply, dim3(M), dim3(256), 0, st, x, ldx, h, ldh, d, eps);
   return hipGetLastError();
 }
 
