@@ -49,6 +49,9 @@ namespace {
 
 constexpr int BG_BM = 256, BG_BN = 256, BG_BK = 64;
 constexpr int BG_EP = 264;   // bf16 row pitch of the staged output tile
+#ifndef BG_EB
+#define BG_EB 8              // residual epilogue: 16-byte chunks per thread loaded at once
+#endif
 constexpr size_t BG_LDS_MAIN = (size_t)2 * (BG_BM + BG_BN) * BG_BK * 2;
 constexpr size_t BG_LDS_EPI = (size_t)BG_BM * BG_EP * 2;
 constexpr size_t BG_LDS = BG_LDS_MAIN > BG_LDS_EPI ? BG_LDS_MAIN : BG_LDS_EPI;
@@ -207,6 +210,56 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     return;
   } else {
     // 16-byte row chunks: chunk q = tid + 256 u is row q >> 5, columns 8 (q & 31)
+    if constexpr (EPI == EPI_RESID_ATTN || EPI == EPI_RESID_MLP) {
+      // x (and x0) of BG_EB chunks loaded at once (rows past M read row M-1,
+      // never stored): loads of 4 chunks at a time left the epilogue waiting
+      // on one latency per 4 chunks
+#pragma unroll 1
+      for (int u0 = 0; u0 < 32; u0 += BG_EB) {
+        uint4 xv[BG_EB], zv[BG_EB];
+#pragma unroll
+        for (int e = 0; e < BG_EB; ++e) {
+          const int q = tid + 256 * (u0 + e);
+          const size_t i = (size_t)min(m0 + (q >> 5), M - 1) * ea.ldr + n0 + (q & 31) * 8;
+          xv[e] = *(const uint4*)(ea.x + i);
+          if constexpr (EPI == EPI_RESID_ATTN) zv[e] = *(const uint4*)(ea.x0 + i);
+        }
+#pragma unroll
+        for (int e = 0; e < BG_EB; ++e) {
+          const int q = tid + 256 * (u0 + e);
+          const int ml = q >> 5, c8 = (q & 31) * 8;
+          const int m = m0 + ml, n = n0 + c8;
+          if (m >= M) continue;
+          const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
+          const uint2 hi = *(const uint2*)(st + ml * BG_EP + c8 + 4);
+          const uint32_t yw[4] = {lo.x, lo.y, hi.x, hi.y};
+          const uint32_t xw[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
+          uint32_t zw[4] = {0u, 0u, 0u, 0u};
+          if constexpr (EPI == EPI_RESID_ATTN) {
+            zw[0] = zv[e].x; zw[1] = zv[e].y; zw[2] = zv[e].z; zw[3] = zv[e].w;
+          }
+          uint32_t o[4];
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            bf16_t r[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float xf = __uint_as_float(h ? (xw[f] & 0xffff0000u) : (xw[f] << 16));
+              const float yf = __uint_as_float(h ? (yw[f] & 0xffff0000u) : (yw[f] << 16));
+              if constexpr (EPI == EPI_RESID_ATTN) {
+                const float zf = __uint_as_float(h ? (zw[f] & 0xffff0000u) : (zw[f] << 16));
+                r[h] = mix_attn(ea.lam, xf, zf, yf);
+              } else {
+                r[h] = mix_mlp(ea.lam, xf, yf);
+              }
+            }
+            o[f] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+          }
+          *(uint4*)(ea.x + (size_t)m * ea.ldr + n) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+      return;
+    }
 #pragma unroll 4
     for (int u = 0; u < 32; ++u) {
       const int q = tid + 256 * u;
@@ -218,40 +271,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
       const uint32_t yw[4] = {lo.x, lo.y, hi.x, hi.y};
       if constexpr (EPI == EPI_STORE) {
         *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      } else if constexpr (EPI == EPI_RELU2) {
+      } else {   // EPI_RELU2
         uint32_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o[e] = (uint32_t)relu2_bf(__uint_as_float(yw[e] << 16)) |
                  ((uint32_t)relu2_bf(__uint_as_float(yw[e] & 0xffff0000u)) << 16);
         *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(o[0], o[1], o[2], o[3]);
-      } else {   // EPI_RESID_ATTN / EPI_RESID_MLP
-        const size_t i = (size_t)m * ea.ldr + n;
-        const uint4 xv = *(const uint4*)(ea.x + i);
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-        uint32_t zw[4] = {0u, 0u, 0u, 0u};
-        if constexpr (EPI == EPI_RESID_ATTN) {
-          const uint4 zv = *(const uint4*)(ea.x0 + i);
-          zw[0] = zv.x; zw[1] = zv.y; zw[2] = zv.z; zw[3] = zv.w;
-        }
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bf16_t r[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float xf = __uint_as_float(h ? (xw[e] & 0xffff0000u) : (xw[e] << 16));
-            const float yf = __uint_as_float(h ? (yw[e] & 0xffff0000u) : (yw[e] << 16));
-            if constexpr (EPI == EPI_RESID_ATTN) {
-              const float zf = __uint_as_float(h ? (zw[e] & 0xffff0000u) : (zw[e] << 16));
-              r[h] = mix_attn(ea.lam, xf, zf, yf);
-            } else {
-              r[h] = mix_mlp(ea.lam, xf, yf);
-            }
-          }
-          o[e] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
-        }
-        *(uint4*)(ea.x + i) = make_uint4(o[0], o[1], o[2], o[3]);
       }
     }
   }
