@@ -1,9 +1,10 @@
 // Large projections y = a @ W^T (W stored (N, K) bf16) of the prefill and the
-// training forward: 256 x 256 output tiles of four waves of 128 x 128, one work-
-// group (one wave per SIMD) per CU, v_mfma_f32_16x16x32_bf16.  The projection
-// routing sends the fc (relu^2) and o-proj (attention residual) projections
-// here (see gemm_big_routes for the measurements); it serves the plain, MLP
-// residual and QKV epilogues as well when called directly.
+// training forward: 256 x 256 (or 256 x 192) output tiles of four waves of
+// 128 x 128 (128 x 96), one work-group (one wave per SIMD) per CU,
+// v_mfma_f32_16x16x32_bf16.  The projection routing sends the fc (relu^2),
+// o-proj (attention residual) and proj (MLP residual) projections here (see
+// gemm_big_routes for the measurements); it serves the plain and QKV
+// epilogues as well when called directly.
 //
 // Main loop (K tiles of 64, two LDS stages, one barrier per K tile):
 //   * the 256 accumulators of a wave live in AGPRs: the MFMA is issued as
@@ -38,6 +39,7 @@
 // Measured against the four prefill shapes (M = 32768) with a plain store:
 // 0.81 / 0.70 / 0.96 / 1.04 PFLOP/s for N x K = 2304 x 768, 768 x 768,
 // 3072 x 768, 768 x 3072 (hipBLASLt: 0.87 / 0.83 / 1.17 / 1.29).
+#include <stdlib.h>
 #include <type_traits>
 #include "common.h"
 #include "epilogue.h"
@@ -47,7 +49,7 @@ namespace ann {
 
 namespace {
 
-constexpr int BG_BM = 256, BG_BN = 256, BG_BK = 64;
+constexpr int BG_BM = 256, BG_BN = 256, BG_BK = 64;   // BG_BN: the widest tile
 constexpr int BG_EP = 264;   // bf16 row pitch of the staged output tile
 #ifndef BG_EB
 #define BG_EB 8              // residual epilogue: 16-byte chunks per thread loaded at once
@@ -93,20 +95,25 @@ __device__ __forceinline__ uint32_t bg_pack_bf16(float a, float b) {
 
 }  // namespace
 
-template <int EPI>
+template <int EPI, int BN>
 __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, const bf16_t* W,
                                                      int M, int N, int K, EpiArgs ea) {
+  static_assert(BN == 256 || BN == 192, "tile width");
+  static_assert(EPI != EPI_QKV || BN == 256, "the QKV epilogue takes 128-column head halves");
+  constexpr int NJ = BN / 32;    // 16-column blocks of a wave (two waves across the tile)
+  constexpr int NWU = BN / 32;   // W chunks per thread and K tile
+  constexpr int CPR = BN / 8;    // 16-byte chunks per output row
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   auto As = [&](int s) { return smem + s * BG_BM * BG_BK; };
-  auto Ws = [&](int s) { return smem + 2 * BG_BM * BG_BK + s * BG_BN * BG_BK; };
+  auto Ws = [&](int s) { return smem + 2 * BG_BM * BG_BK + s * BN * BG_BK; };
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv >> 1, wn = wv & 1;
-  const int ntm = (M + BG_BM - 1) / BG_BM, ntn = N / BG_BN, nt = ntm * ntn;
+  const int ntm = (M + BG_BM - 1) / BG_BM, ntn = N / BN, nt = ntm * ntn;
   const int per = (nt + 7) / 8;
   const int t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   if (t >= nt) return;
   const int tm = t / ntn, tn = t % ntn;
-  const int m0 = tm * BG_BM, n0 = tn * BG_BN;
+  const int m0 = tm * BG_BM, n0 = tn * BN;
   const int KT = K / BG_BK;
 
   // staged K-tile chunks: chunk g of a thread is operand g & 1 (A, W), row
@@ -117,20 +124,20 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     const int row = crow + 32 * u;
     if (op == 0)
       ra[u] = *(const bg_u32x4*)(A + (size_t)min(m0 + row, M - 1) * lda + kt * BG_BK + cc * 8);
-    else
+    else if (u < NWU)
       rw[u] = *(const bg_u32x4*)(W + (size_t)(n0 + row) * K + kt * BG_BK + cc * 8);
   };
   auto lstore1 = [&](int op, int u, int s) {
     const int row = crow + 32 * u;
     if (op == 0) *(bg_u32x4*)(As(s) + bg_off(row, cc)) = ra[u];
-    else *(bg_u32x4*)(Ws(s) + bg_off(row, cc)) = rw[u];
+    else if (u < NWU) *(bg_u32x4*)(Ws(s) + bg_off(row, cc)) = rw[u];
   };
 
-  bg_floatx4 acc[8][8];
+  bg_floatx4 acc[8][NJ];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = (bg_floatx4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = (bg_floatx4){0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15, kg = lane >> 4;
 
   // prologue: tile 0 into stage 0, tile 1 (clamped) in flight in the
@@ -155,23 +162,23 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
   for (int kt = 0; kt < KT; ++kt) {
     const int s = kt & 1;
     const bf16_t* as = As(s) + (wm * 128 + r16) * BG_BK;
-    const bf16_t* ws = Ws(s) + (wn * 128 + r16) * BG_BK;
+    const bf16_t* ws = Ws(s) + (wn * (BN / 2) + r16) * BG_BK;
     const int ch0 = kg ^ ((r16 >> 1) & 7), ch1 = (4 + kg) ^ ((r16 >> 1) & 7);
     const bg_lds_char* pa0 = (const bg_lds_char*)(as + (ch0 << 3));
     const bg_lds_char* pa1 = (const bg_lds_char*)(as + (ch1 << 3));
     const bg_lds_char* pb0 = (const bg_lds_char*)(ws + (ch0 << 3));
     const bg_lds_char* pb1 = (const bg_lds_char*)(ws + (ch1 << 3));
-    bg_bf16x8 b0[8], b1[8];
-    bg_static_for<0, 8>([&](auto jc) __attribute__((always_inline)) {
+    bg_bf16x8 b0[NJ], b1[NJ];
+    bg_static_for<0, NJ>([&](auto jc) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value;
       b0[j] = bg_lds_read<j * 16 * BG_BK * 2>(pb0);
     });
     bg_bf16x8 a = bg_lds_read<0>(pa0);
-    bg_static_for<0, 8>([&](auto jc) __attribute__((always_inline)) {
+    bg_static_for<0, NJ>([&](auto jc) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value;
       b1[j] = bg_lds_read<j * 16 * BG_BK * 2>(pb1);
     });
-    bg_wait_lgkm<8>();   // b0 and a; the eight b1 reads may still fly
+    bg_wait_lgkm<NJ>();   // b0 and a; the b1 reads may still fly
     bg_static_for<0, 16>([&](auto gc) __attribute__((always_inline)) {
       constexpr int g = decltype(gc)::value;
       constexpr int i = g & 7, kh = g >> 3;
@@ -185,7 +192,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
       gload1(g & 1, g >> 1, min(kt + 2, KT - 1));
       asm volatile("" ::: "memory");
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bg_mfma(acc[i][j], kh ? b1[j] : b0[j], a);
+      for (int j = 0; j < NJ; ++j) bg_mfma(acc[i][j], kh ? b1[j] : b0[j], a);
       if constexpr (g < 15) bg_wait_lgkm<0>();
       a = an;
     });
@@ -197,8 +204,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int ml = wm * 128 + i * 16 + r16, nl = wn * 128 + j * 16 + 4 * kg;
+    for (int j = 0; j < NJ; ++j) {
+      const int ml = wm * 128 + i * 16 + r16, nl = wn * (BN / 2) + j * 16 + 4 * kg;
       const bg_floatx4 v = acc[i][j];
       *(uint2*)(st + ml * BG_EP + nl) = make_uint2(bg_pack_bf16(v[0], v[1]), bg_pack_bf16(v[2], v[3]));
     }
@@ -209,25 +216,26 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     qkv_tile_epilogue<BG_BM, BG_EP>(ea, st + 128, m0, n0 + 128, M, tid);
     return;
   } else {
-    // 16-byte row chunks: chunk q = tid + 256 u is row q >> 5, columns 8 (q & 31)
+    // 16-byte row chunks: chunk q = tid + 256 u is row q / CPR, columns 8 (q % CPR)
     if constexpr (EPI == EPI_RESID_ATTN || EPI == EPI_RESID_MLP) {
       // x (and x0) of BG_EB chunks loaded at once (rows past M read row M-1,
       // never stored): loads of 4 chunks at a time left the epilogue waiting
       // on one latency per 4 chunks
+      static_assert(CPR % BG_EB == 0, "whole batches");
 #pragma unroll 1
-      for (int u0 = 0; u0 < 32; u0 += BG_EB) {
+      for (int u0 = 0; u0 < CPR; u0 += BG_EB) {
         uint4 xv[BG_EB], zv[BG_EB];
 #pragma unroll
         for (int e = 0; e < BG_EB; ++e) {
           const int q = tid + 256 * (u0 + e);
-          const size_t i = (size_t)min(m0 + (q >> 5), M - 1) * ea.ldr + n0 + (q & 31) * 8;
+          const size_t i = (size_t)min(m0 + q / CPR, M - 1) * ea.ldr + n0 + (q % CPR) * 8;
           xv[e] = *(const uint4*)(ea.x + i);
           if constexpr (EPI == EPI_RESID_ATTN) zv[e] = *(const uint4*)(ea.x0 + i);
         }
 #pragma unroll
         for (int e = 0; e < BG_EB; ++e) {
           const int q = tid + 256 * (u0 + e);
-          const int ml = q >> 5, c8 = (q & 31) * 8;
+          const int ml = q / CPR, c8 = (q % CPR) * 8;
           const int m = m0 + ml, n = n0 + c8;
           if (m >= M) continue;
           const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
@@ -261,9 +269,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
       return;
     }
 #pragma unroll 4
-    for (int u = 0; u < 32; ++u) {
+    for (int u = 0; u < CPR; ++u) {
       const int q = tid + 256 * u;
-      const int ml = q >> 5, c8 = (q & 31) * 8;
+      const int ml = q / CPR, c8 = (q % CPR) * 8;
       const int m = m0 + ml, n = n0 + c8;
       if (m >= M) continue;
       const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
@@ -284,21 +292,52 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
 }
 
 // Whether the projection routing (gemm()) sends (epi, M, N, K) here.  In the
-// 64 x 512-token prefill, against the two-work-groups-per-CU tiles of
-// k_gemm_2w (rocprof): fc (relu^2) 182 against 190 us and o-proj (attention
-// residual) 103 against 108 us go here; qkv (170 against 151 us) and proj
-// (MLP residual, 197 against 193 us) do not -- with one work-group per CU the
-// heavier epilogues (QK-norm / RoPE / cache writes, x read and written) are
-// not overlapped by another work-group's MFMAs.  The kernel still serves
-// every epilogue of gemm_big() when called directly.
-bool gemm_big_routes(int epi) { return epi == EPI_RELU2 || epi == EPI_RESID_ATTN; }
+// 64 x 512-token prefill, per layer against the two-work-groups-per-CU tiles
+// of k_gemm_2w (rocprof, one box): fc (relu^2) 185 us here; o-proj (attention
+// residual) 79 us here with 192-column tiles (103 with 256, 108 in k_gemm_2w);
+// proj (MLP residual) 159 us here with 192-column tiles against 199 in
+// k_gemm_2w; qkv 173 us here against 155 in k_gemm_2w -- its QK-norm / RoPE /
+// cache-write epilogue is not overlapped by another work-group's MFMAs at one
+// work-group per CU.  The kernel still serves every epilogue of gemm_big()
+// when called directly.
+bool gemm_big_routes(int epi) {
+  return epi == EPI_RELU2 || epi == EPI_RESID_ATTN || epi == EPI_RESID_MLP;
+}
 
-// Whether gemm_big can take (epi, M, N, K): whole 256-column tiles, 64-deep K
-// tiles, 16-byte aligned rows and outputs, and enough tiles (at least 96) for
-// the one-work-group-per-CU kernel to fill the chip.
+// Tile width for an M x N output: 256 or 192 columns, whichever needs fewer
+// CU-rounds times columns (one work-group per CU).  N = 768 at M = 32768:
+// 384 tiles of 256 fill 1.5 rounds of 256 CUs, 512 tiles of 192 two whole
+// rounds of three-quarter tiles.  The QKV epilogue needs 256 (head halves).
+// ANN_GEMM_BIG_BN=256 / 192 forces one where it divides N (read once per
+// process).
+static int big_bn(int epi, int M, int N) {
+  static int cus = 0, force = -1;
+  if (force < 0) {
+    const char* e = getenv("ANN_GEMM_BIG_BN");
+    force = e ? atoi(e) : 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  const bool ok192 = epi != EPI_QKV && N % 192 == 0, ok256 = N % 256 == 0;
+  if (!ok192) return 256;
+  if (!ok256) return 192;
+  if (force == 192 || force == 256) return force;
+  const long long ntm = (M + BG_BM - 1) / BG_BM;
+  auto cost = [&](int bn) { return (ntm * (N / bn) + cus - 1) / cus * bn; };
+  return cost(192) < cost(256) ? 192 : 256;
+}
+
+// Whether gemm_big can take (epi, M, N, K): whole 256- or 192-column tiles,
+// 64-deep K tiles, 16-byte aligned rows and outputs, and enough tiles (at
+// least 96) for the one-work-group-per-CU kernel to fill the chip.
 bool gemm_big_fits(int epi, const bf16_t* A, int lda, int M, int N, int K, const EpiArgs& ea) {
-  if (M < 512 || N % BG_BN || K % BG_BK || K < BG_BK || lda % 8 || ((uintptr_t)A & 15)) return false;
-  if ((long long)((M + BG_BM - 1) / BG_BM) * (N / BG_BN) < 96) return false;
+  if (M < 512 || N % 64 || K % BG_BK || K < BG_BK || lda % 8 || ((uintptr_t)A & 15)) return false;
+  const int bn = big_bn(epi, M, N);
+  if (N % bn) return false;
+  if ((long long)((M + BG_BM - 1) / BG_BM) * (N / bn) < 96) return false;
   switch (epi) {
     case EPI_STORE:
     case EPI_RELU2:
@@ -315,32 +354,39 @@ bool gemm_big_fits(int epi, const bf16_t* A, int lda, int M, int N, int K, const
   }
 }
 
-template <int EPI>
+template <int EPI, int BN>
 static hipError_t launch_big(const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                              const EpiArgs& ea, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_big<EPI>,
+    const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_big<EPI, BN>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              (int)BG_LDS);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const int nt = ((M + BG_BM - 1) / BG_BM) * (N / BG_BN);
+  const int nt = ((M + BG_BM - 1) / BG_BM) * (N / BN);
   const int grid = (nt + 7) / 8 * 8;
-  hipLaunchKernelGGL(k_gemm_big<EPI>, dim3(grid), dim3(256), BG_LDS, st, A, lda, W, M, N, K, ea);
+  hipLaunchKernelGGL((k_gemm_big<EPI, BN>), dim3(grid), dim3(256), BG_LDS, st, A, lda, W, M, N, K,
+                     ea);
   return hipGetLastError();
 }
 
 hipError_t gemm_big(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                     const EpiArgs& ea, hipStream_t st) {
   if (!gemm_big_fits(epi, A, lda, M, N, K, ea)) return hipErrorInvalidValue;
+  const bool w192 = big_bn(epi, M, N) == 192;
   switch (epi) {
-    case EPI_STORE: return launch_big<EPI_STORE>(A, lda, W, M, N, K, ea, st);
-    case EPI_RELU2: return launch_big<EPI_RELU2>(A, lda, W, M, N, K, ea, st);
-    case EPI_RESID_ATTN: return launch_big<EPI_RESID_ATTN>(A, lda, W, M, N, K, ea, st);
-    case EPI_RESID_MLP: return launch_big<EPI_RESID_MLP>(A, lda, W, M, N, K, ea, st);
-    case EPI_QKV: return launch_big<EPI_QKV>(A, lda, W, M, N, K, ea, st);
+#define ANN_BIG_CASE(E)                                                              \
+  case E:                                                                            \
+    return w192 ? launch_big<E, 192>(A, lda, W, M, N, K, ea, st)                     \
+                : launch_big<E, 256>(A, lda, W, M, N, K, ea, st);
+    ANN_BIG_CASE(EPI_STORE)
+    ANN_BIG_CASE(EPI_RELU2)
+    ANN_BIG_CASE(EPI_RESID_ATTN)
+    ANN_BIG_CASE(EPI_RESID_MLP)
+#undef ANN_BIG_CASE
+    case EPI_QKV: return launch_big<EPI_QKV, 256>(A, lda, W, M, N, K, ea, st);
     default: return hipErrorInvalidValue;
   }
 }
