@@ -305,9 +305,12 @@ bool gemm_big_routes(int epi) {
 }
 
 // Tile width for an M x N output: 256 or 192 columns, whichever needs fewer
-// CU-rounds times columns (one work-group per CU).  N = 768 at M = 32768:
-// 384 tiles of 256 fill 1.5 rounds of 256 CUs, 512 tiles of 192 two whole
-// rounds of three-quarter tiles.  The QKV epilogue needs 256 (head halves).
+// CU-rounds times columns (one work-group per CU), a 192-column tile counted
+// 15% dearer per column (less reuse of each A tile: the cfg4 fc shape, 480 x 16
+// tiles of 192 against 480 x 12 of 256, measured 818 against 713 us).  N = 768
+// at M = 32768: 384 tiles of 256 fill 1.5 rounds of 256 CUs, 512 tiles of 192
+// two whole rounds (o-proj 79 against 103 us).  The QKV epilogue needs 256
+// (head halves).
 // ANN_GEMM_BIG_BN=256 / 192 forces one where it divides N (read once per
 // process).
 static int big_bn(int epi, int M, int N) {
@@ -326,8 +329,8 @@ static int big_bn(int epi, int M, int N) {
   if (!ok256) return 192;
   if (force == 192 || force == 256) return force;
   const long long ntm = (M + BG_BM - 1) / BG_BM;
-  auto cost = [&](int bn) { return (ntm * (N / bn) + cus - 1) / cus * bn; };
-  return cost(192) < cost(256) ? 192 : 256;
+  auto rounds = [&](int bn) { return (ntm * (N / bn) + cus - 1) / cus; };
+  return rounds(192) * 192 * 115 < rounds(256) * 256 * 100 ? 192 : 256;
 }
 
 // Whether gemm_big can take (epi, M, N, K): whole 256- or 192-column tiles,
