@@ -180,6 +180,31 @@ def test_forward_loss_matches_oracle(dh, V, B, T):
     assert abs(mean.item() - rows.mean().item()) < 1e-5
 
 
+@pytest.mark.parametrize("V", [50304, 16384])
+def test_forward_loss_large_vocab_equals_cross_entropy_of_own_logits(V):
+    """The fused CE epilogue at the model's vocabulary (393 column tiles of 128,
+    the last partial) and at 1024 rows, against torch cross_entropy over the
+    same engine's softcapped logits."""
+    cfg = GPTConfig(vocab_size=V, num_layers=2, num_heads=2, model_dim=256, seq_len=512,
+                    window=100, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 41, dense=True))
+    rng = np.random.default_rng(V)
+    B, T = 2, 512
+    tok = rng.integers(0, V, (B, T))
+    tgt = rng.integers(0, V, (B, T))
+    tgt[0, 0], tgt[-1, -1] = 0, V - 1
+    print(f"case V={V} B={B} T={T}", flush=True)
+    eng = _engine(cfg, p, B)
+    lg = eng.forward_logits(tok).double()
+    ref = torch.nn.functional.cross_entropy(lg.reshape(-1, V),
+                                            torch.from_numpy(tgt).reshape(-1).cuda(),
+                                            reduction="none")
+    del lg
+    mean, rows = eng.forward_loss(tok, tgt, rows=True)
+    assert (rows.double() - ref).abs().max().item() < 1e-4
+    assert abs(mean.item() - ref.mean().item()) < 1e-5
+
+
 def test_forward_loss_equals_cross_entropy_of_own_logits():
     """Without the oracle: the fused CE epilogue equals torch cross_entropy
     over the same engine's (B, T, V) softcapped logits (same z, only the
