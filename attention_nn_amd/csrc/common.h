@@ -102,6 +102,31 @@ __device__ __forceinline__ bf16_t relu2_bf(float y) {
   const float r = u > 0.f ? u : 0.f;
   return f2bf(r * r);
 }
+// mix_attn / mix_mlp of two bf16 pairs packed in words (y already bf16),
+// each eager rounding done as one packed conversion of the pair.
+__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t mix_attn_pair(const float* lam, uint32_t x, uint32_t x0,
+                                                  uint32_t y) {
+  const uint32_t a = pack2(lam[0] * lo_f(x), lam[0] * hi_f(x));
+  const uint32_t b = pack2(lam[2] * lo_f(y), lam[2] * hi_f(y));
+  const uint32_t t = pack2(lo_f(a) + lo_f(b), hi_f(a) + hi_f(b));
+  const uint32_t c = pack2(lam[4] * lo_f(x0), lam[4] * hi_f(x0));
+  return pack2(lo_f(t) + lo_f(c), hi_f(t) + hi_f(c));
+}
+__device__ __forceinline__ uint32_t mix_mlp_pair(const float* lam, uint32_t x, uint32_t y) {
+  const uint32_t a = pack2(lam[1] * lo_f(x), lam[1] * hi_f(x));
+  const uint32_t b = pack2(lam[3] * lo_f(y), lam[3] * hi_f(y));
+  return pack2(lo_f(a) + lo_f(b), hi_f(a) + hi_f(b));
+}
+// relu2_bf of two values as one packed word: bf16(max(y, 0)) equals
+// max(bf16(y), 0) (rounding is monotone and keeps 0; NaN gives 0 on both
+// sides), so the clamp goes first and each pair takes two packed conversions.
+__device__ __forceinline__ uint32_t relu2_pair(float y0, float y1) {
+  const uint32_t u = pack2(fmaxf(y0, 0.f), fmaxf(y1, 0.f));
+  const float a = __uint_as_float(u << 16), b = __uint_as_float(u & 0xffff0000u);
+  return pack2(a * a, b * b);
+}
 // Order-preserving 16-bit key of a bf16 value (greedy argmax).
 __device__ __forceinline__ uint32_t zkey(bf16_t h) {
   return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);

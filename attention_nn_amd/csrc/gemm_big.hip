@@ -29,11 +29,16 @@
 //     16-row fragment reads.
 // The MFMA operands are swapped (C^T = W A^T) so that a lane holds four
 // consecutive columns of one row.  Epilogue: the tile is rounded to bf16 (every
-// epilogue here starts from bf16(y), as the reference's eager ops do) into LDS
-// (row pitch 264: the 8-byte writes of 16 rows spread over the banks), then
-// each thread handles 16-byte row chunks: plain / relu^2 stores, the residual
-// mixes (x, x0 read and x written as 16-byte words), or the QKV epilogue of
-// each 128-column half (QK-norm, RoPE, q and KV-cache writes).  Work-group i
+// epilogue here starts from bf16(y), as the reference's eager ops do; relu^2
+// is applied at this point) into LDS (row pitch 264: the 8-byte writes of 16
+// rows spread over the banks), then each thread handles 16-byte row chunks:
+// plain / relu^2 copies, the residual mixes (x, x0 read and x written as
+// 16-byte words, the first batch loaded before the staging), or the QKV
+// epilogue of each 128-column half (QK-norm, RoPE, q and KV-cache writes).
+// With one wave per SIMD nothing hides the epilogue's VALU work, so every
+// eager rounding is a packed pair conversion (v_cvt_pk_bf16_f32): per-work-
+// group stamps of the 64 x 512-token prefill put the fc epilogue at 5.7-7.5
+// us per tile after this, 7.3 before (main loop ~21 us).  Work-group i
 // runs on XCD i % 8; each XCD takes a contiguous range of tiles, N-fastest, so
 // the N tiles of an M block share its A rows in that XCD's L2.
 // Measured against the four prefill shapes (M = 32768) with a plain store:
@@ -89,11 +94,8 @@ __device__ __forceinline__ void bg_wait_lgkm() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
 
-__device__ __forceinline__ uint32_t bg_pack_bf16(float a, float b) {
-  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-}
-
 }  // namespace
+
 
 template <int EPI, int BN>
 __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, const bf16_t* W,
@@ -199,6 +201,22 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     __syncthreads();
   }
 
+  // residual epilogues: x (and x0) chunks of the first batch loaded before the
+  // staging (chunk q = tid + 256 u is row q / CPR, columns 8 (q % CPR); rows
+  // past M read row M - 1 and are never stored)
+  constexpr bool RES = EPI == EPI_RESID_ATTN || EPI == EPI_RESID_MLP;
+  static_assert(!RES || CPR % BG_EB == 0, "whole batches");
+  bg_u32x4 xv[2][BG_EB], zv[2][BG_EB];
+  auto res_load = [&](int b) {
+#pragma unroll
+    for (int e = 0; e < BG_EB; ++e) {
+      const int q = tid + 256 * (b * BG_EB + e);
+      const size_t i = (size_t)min(m0 + q / CPR, M - 1) * ea.ldr + n0 + (q % CPR) * 8;
+      xv[b & 1][e] = *(const bg_u32x4*)(ea.x + i);
+      if constexpr (EPI == EPI_RESID_ATTN) zv[b & 1][e] = *(const bg_u32x4*)(ea.x0 + i);
+    }
+  };
+  if constexpr (RES) res_load(0);
   // ---- stage bf16(y): lane holds row m = block row + r16, columns 4 kg ..
   bf16_t* st = smem;
 #pragma unroll
@@ -207,7 +225,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     for (int j = 0; j < NJ; ++j) {
       const int ml = wm * 128 + i * 16 + r16, nl = wn * (BN / 2) + j * 16 + 4 * kg;
       const bg_floatx4 v = acc[i][j];
-      *(uint2*)(st + ml * BG_EP + nl) = make_uint2(bg_pack_bf16(v[0], v[1]), bg_pack_bf16(v[2], v[3]));
+      uint2 w;
+      if constexpr (EPI == EPI_RELU2)   // relu^2 applied here: the copy below only moves bytes
+        w = make_uint2(relu2_pair(v[0], v[1]), relu2_pair(v[2], v[3]));
+      else
+        w = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+      *(uint2*)(st + ml * BG_EP + nl) = w;
     }
   __syncthreads();
 
@@ -217,75 +240,52 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     return;
   } else {
     // 16-byte row chunks: chunk q = tid + 256 u is row q / CPR, columns 8 (q % CPR)
-    if constexpr (EPI == EPI_RESID_ATTN || EPI == EPI_RESID_MLP) {
-      // x (and x0) of BG_EB chunks loaded at once (rows past M read row M-1,
-      // never stored): loads of 4 chunks at a time left the epilogue waiting
-      // on one latency per 4 chunks
-      static_assert(CPR % BG_EB == 0, "whole batches");
-#pragma unroll 1
-      for (int u0 = 0; u0 < CPR; u0 += BG_EB) {
-        uint4 xv[BG_EB], zv[BG_EB];
+    if constexpr (RES) {
+      // batch b + 1's loads fly while batch b is mixed and stored
+      float lam[5];
+#pragma unroll
+      for (int e = 0; e < 5; ++e) lam[e] = ea.lam[e];
+#pragma unroll
+      for (int b = 0; b < CPR / BG_EB; ++b) {
+        if (b + 1 < CPR / BG_EB) res_load(b + 1);
 #pragma unroll
         for (int e = 0; e < BG_EB; ++e) {
-          const int q = tid + 256 * (u0 + e);
-          const size_t i = (size_t)min(m0 + q / CPR, M - 1) * ea.ldr + n0 + (q % CPR) * 8;
-          xv[e] = *(const uint4*)(ea.x + i);
-          if constexpr (EPI == EPI_RESID_ATTN) zv[e] = *(const uint4*)(ea.x0 + i);
-        }
-#pragma unroll
-        for (int e = 0; e < BG_EB; ++e) {
-          const int q = tid + 256 * (u0 + e);
+          const int q = tid + 256 * (b * BG_EB + e);
           const int ml = q / CPR, c8 = (q % CPR) * 8;
-          const int m = m0 + ml, n = n0 + c8;
-          if (m >= M) continue;
-          const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
-          const uint2 hi = *(const uint2*)(st + ml * BG_EP + c8 + 4);
-          const uint32_t yw[4] = {lo.x, lo.y, hi.x, hi.y};
-          const uint32_t xw[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
-          uint32_t zw[4] = {0u, 0u, 0u, 0u};
-          if constexpr (EPI == EPI_RESID_ATTN) {
-            zw[0] = zv[e].x; zw[1] = zv[e].y; zw[2] = zv[e].z; zw[3] = zv[e].w;
-          }
-          uint32_t o[4];
+          const bg_u32x4 y = *(const bg_u32x4*)(st + ml * BG_EP + c8);
+          const bg_u32x4 x = xv[b & 1][e];
+          bg_u32x4 o;
 #pragma unroll
           for (int f = 0; f < 4; ++f) {
-            bf16_t r[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const float xf = __uint_as_float(h ? (xw[f] & 0xffff0000u) : (xw[f] << 16));
-              const float yf = __uint_as_float(h ? (yw[f] & 0xffff0000u) : (yw[f] << 16));
-              if constexpr (EPI == EPI_RESID_ATTN) {
-                const float zf = __uint_as_float(h ? (zw[f] & 0xffff0000u) : (zw[f] << 16));
-                r[h] = mix_attn(ea.lam, xf, zf, yf);
-              } else {
-                r[h] = mix_mlp(ea.lam, xf, yf);
-              }
-            }
-            o[f] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+            if constexpr (EPI == EPI_RESID_ATTN) o[f] = mix_attn_pair(lam, x[f], zv[b & 1][e][f], y[f]);
+            else o[f] = mix_mlp_pair(lam, x[f], y[f]);
           }
-          *(uint4*)(ea.x + (size_t)m * ea.ldr + n) = make_uint4(o[0], o[1], o[2], o[3]);
+          if (m0 + ml < M) *(bg_u32x4*)(ea.x + (size_t)(m0 + ml) * ea.ldr + n0 + c8) = o;
         }
       }
       return;
     }
-#pragma unroll 4
-    for (int u = 0; u < CPR; ++u) {
-      const int q = tid + 256 * u;
-      const int ml = q / CPR, c8 = (q % CPR) * 8;
-      const int m = m0 + ml, n = n0 + c8;
-      if (m >= M) continue;
-      const uint2 lo = *(const uint2*)(st + ml * BG_EP + c8);
-      const uint2 hi = *(const uint2*)(st + ml * BG_EP + c8 + 4);
-      const uint32_t yw[4] = {lo.x, lo.y, hi.x, hi.y};
-      if constexpr (EPI == EPI_STORE) {
-        *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      } else {   // EPI_RELU2
-        uint32_t o[4];
+    // plain / relu^2 (already applied): 16-byte row chunks, eight LDS reads
+    // in flight per thread; the fc output goes out with non-temporal stores
+    // (it is read back only by the next projection; 10 us less per fc call)
+    static_assert(CPR % 8 == 0, "whole batches");
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = (uint32_t)relu2_bf(__uint_as_float(yw[e] << 16)) |
-                 ((uint32_t)relu2_bf(__uint_as_float(yw[e] & 0xffff0000u)) << 16);
-        *(uint4*)(ea.out + (size_t)m * ea.ldo + n) = make_uint4(o[0], o[1], o[2], o[3]);
+    for (int u0 = 0; u0 < CPR; u0 += 8) {
+      bg_u32x4 w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int q = tid + 256 * (u0 + e);
+        w[e] = *(const bg_u32x4*)(st + (q / CPR) * BG_EP + (q % CPR) * 8);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int q = tid + 256 * (u0 + e);
+        const int m = m0 + q / CPR, n = n0 + (q % CPR) * 8;
+        if (m < M) {
+          bg_u32x4* dst = (bg_u32x4*)(ea.out + (size_t)m * ea.ldo + n);
+          if constexpr (EPI == EPI_RELU2) __builtin_nontemporal_store(w[e], dst);
+          else *dst = w[e];
+        }
       }
     }
   }
@@ -395,3 +395,4 @@ hipError_t gemm_big(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, i
 }
 
 }  // namespace ann
+
