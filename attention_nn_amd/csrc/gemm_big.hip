@@ -217,6 +217,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
     }
   };
   if constexpr (RES) res_load(0);
+  QkvRows<BG_BM> pr;
+  if constexpr (EPI == EPI_QKV) qkv_prefetch<BG_BM>(ea, m0, M, tid, pr);
   // ---- stage bf16(y): lane holds row m = block row + r16, columns 4 kg ..
   bf16_t* st = smem;
 #pragma unroll
@@ -235,8 +237,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
   __syncthreads();
 
   if constexpr (EPI == EPI_QKV) {
-    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st, m0, n0, M, tid);
-    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st + 128, m0, n0 + 128, M, tid);
+    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st, m0, n0, M, tid, pr);
+    qkv_tile_epilogue<BG_BM, BG_EP>(ea, st + 128, m0, n0 + 128, M, tid, pr);
     return;
   } else {
     // 16-byte row chunks: chunk q = tid + 256 u is row q / CPR, columns 8 (q % CPR)

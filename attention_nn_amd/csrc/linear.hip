@@ -613,6 +613,8 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
       }
     }
   } else if constexpr (EPI == EPI_QKV) {
+    QkvRows<BM> pr;
+    qkv_prefetch<BM>(ea, m0, M, tid, pr);
     __syncthreads();   // every wave is done with the last K tile in LDS
     constexpr int CP = BN + 8;
 #pragma unroll
@@ -624,7 +626,7 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
             make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     __syncthreads();
-    qkv_tile_epilogue<BM, GM_BN + 8>(ea, smem, m0, n0, M, tid);
+    qkv_tile_epilogue<BM, GM_BN + 8>(ea, smem, m0, n0, M, tid, pr);
   } else {
     const bool vec = epi_vec_ok<EPI>(ea);
 #pragma unroll
