@@ -37,6 +37,7 @@
 // Dh/8 lanes x 8 dims per V row for P.V; a ring of three chunks is in flight
 // per wave.  The four waves' (O, L) are summed once through LDS in wave order.
 #include <math.h>
+#include <stdlib.h>
 #include "common.h"
 #include "launch.h"
 
@@ -44,7 +45,6 @@ namespace ann {
 
 constexpr int AD_THREADS = 256;
 constexpr int AD_KW = 16;    // keys per wave chunk
-constexpr int AD_RING = 3;   // chunks in flight per wave
 
 typedef __bf16 ad_bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -83,8 +83,12 @@ __device__ __forceinline__ void weight_prefetch(const uint4* __restrict__ p, siz
   if (f == AD_PF_MAGIC) *sink = f;
 }
 
-template <int DH>
-__global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
+// RING chunks in flight per wave.  RING 3 takes 195 VGPRs (two work-groups
+// per CU); RING 2 is held to 128 (four per CU) for grids of many (b, h)
+// work-groups, which then run in fewer rounds.
+template <int DH, int RING>
+__global__ __launch_bounds__(AD_THREADS) __attribute__((amdgpu_waves_per_eu(RING == 2 ? 3 : 1)))
+void k_attn_dec(
     const bf16_t* __restrict__ qkv, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
     u64* __restrict__ part, unsigned* __restrict__ cnt, unsigned* __restrict__ err,
@@ -147,9 +151,9 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
                                     : make_uint4(0, 0, 0, 0);
     }
   };
-  uint4 kb[AD_RING][KU], vb[AD_RING][VU];
+  uint4 kb[RING][KU], vb[RING][VU];
 #pragma unroll
-  for (int r = 0; r < AD_RING - 1; ++r)
+  for (int r = 0; r < RING - 1; ++r)
     if (r < nt) load(r, kb[r], vb[r]);   // independent of q: overlaps the prologue
 
   // ---- new token: QK-norm + RoPE (wave 0, one dim pair per lane)
@@ -229,12 +233,12 @@ __global__ __launch_bounds__(AD_THREADS) void k_attn_dec(
     }
   };
 
-  for (int t = 0; t < nt; t += AD_RING) {
+  for (int t = 0; t < nt; t += RING) {
 #pragma unroll
-    for (int r = 0; r < AD_RING; ++r) {
+    for (int r = 0; r < RING; ++r) {
       if (t + r < nt) {
-        const int tn = t + r + AD_RING - 1;
-        if (tn < nt) load(tn, kb[(r + AD_RING - 1) % AD_RING], vb[(r + AD_RING - 1) % AD_RING]);
+        const int tn = t + r + RING - 1;
+        if (tn < nt) load(tn, kb[(r + RING - 1) % RING], vb[(r + RING - 1) % RING]);
         compute(t + r, kb[r], vb[r]);
       }
     }
@@ -319,20 +323,33 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
   dim3 grid(nsplit, H, B + (pfon ? pf.slices : 0));
   const uint4* pfp = pfon ? (const uint4*)pf.p : nullptr;
   const size_t pfn = pfon ? pf.bytes / 16 : 0;
+  // more than two (b, h, split) work-groups per CU: the 128-VGPR form
+  static int cus = 0, force = -1;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    const char* e = getenv("ANN_ATTN_RING");
+    force = e ? atoi(e) : 0;
+  }
+  const bool r2 = force == 2 || (force != 3 && (long long)nsplit * H * B > 2LL * cus);
+#define ANN_AD(D, R)                                                                         \
+  hipLaunchKernelGGL((k_attn_dec<D, R>), grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn, \
+                     part, cnt, err, out, H, max_ctx, window, (int)long_layer, scale, shift, eps, \
+                     nsplit, B, pfp, pfn, pf.sink)
   switch (Dh) {
     case 64:
-      hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
-                         part, cnt, err, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
-                         nsplit, B, pfp, pfn, pf.sink);
+      if (r2) ANN_AD(64, 2); else ANN_AD(64, 3);
       break;
     case 128:
-      hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn,
-                         part, cnt, err, out, H, max_ctx, window, (int)long_layer, scale, shift, eps,
-                         nsplit, B, pfp, pfn, pf.sink);
+      if (r2) ANN_AD(128, 2); else ANN_AD(128, 3);
       break;
     default:
       return hipErrorInvalidValue;
   }
+#undef ANN_AD
   return hipGetLastError();
 }
 
