@@ -423,9 +423,12 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   // the QKV and CE epilogues work on 128-column tiles (whole heads; the
   // per-tile partial sums of the loss)
   static_assert((EPI != EPI_QKV && EPI != EPI_CE) || BN == GM_BN, "128-column tiles");
-  constexpr int SMEM = (BM + BN) * GM_BK > (EPI == EPI_QKV ? BM * (GM_BN + 8) : 0)
+  // staged epilogues (QKV; PE_B / PE_X on full tiles) reuse the LDS for a bf16
+  // BM x BN tile of row pitch BN + 8
+  constexpr bool STAGED = EPI == EPI_QKV || EPI == EPI_PE_B || EPI == EPI_PE_X;
+  constexpr int SMEM = (BM + BN) * GM_BK > (STAGED ? BM * (BN + 8) : 0)
                            ? (BM + BN) * GM_BK
-                           : BM * (GM_BN + 8);
+                           : BM * (BN + 8);
   __shared__ __attribute__((aligned(16))) bf16_t smem[SMEM];
   bf16_t* As = smem;
   bf16_t* Bs = smem + BM * GM_BK;
@@ -628,6 +631,81 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
     __syncthreads();
     qkv_tile_epilogue<BM, GM_BN + 8>(ea, smem, m0, n0, M, tid, pr);
   } else {
+    if constexpr (EPI == EPI_PE_B || EPI == EPI_PE_X) {
+      // full tiles with 16-byte rows: x prefetched before the staging
+      // barrier, bf16(y) staged in LDS (exact: both epilogues start from
+      // bf16(y)), 16-byte row chunks mixed and stored, and for PE_X the
+      // transposed copy written from LDS as 16-byte column runs.  Measured
+      // against per-lane 8-byte accesses and 2-byte transposed stores.
+      const bool full = m0 + BM <= M && n0 + BN <= N && ((ea.ldr | ea.ldo) & 7) == 0 &&
+                        (((uintptr_t)ea.x | (uintptr_t)ea.out) & 15) == 0 &&
+                        (EPI != EPI_PE_X || !ea.outT ||
+                         ((ea.ldoT & 7) == 0 && ((uintptr_t)ea.outT & 15) == 0));
+      if (full) {
+        constexpr int CP = BN + 8, CPR = BN / 8, NCH = BM * CPR / 256;
+        static_assert(BM * CPR % 256 == 0, "whole chunks per thread");
+        uint4 xv[NCH];
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+          const int q = tid + 256 * u;
+          xv[u] = *(const uint4*)(ea.x + (size_t)(m0 + q / CPR) * ea.ldr + n0 + (q % CPR) * 8);
+        }
+        __syncthreads();   // every wave is done with the last K tile in LDS
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const floatx4_t y = acc[j][i];
+            *(uint2*)(smem + (wm * WM + i * 16 + r16) * CP + wn * WN + j * 16 + (lane >> 4) * 4) =
+                make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+          }
+        __syncthreads();
+        const float s0 = ea.s0, s1 = ea.s1;
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+          const int q = tid + 256 * u, ml = q / CPR, c8 = (q % CPR) * 8;
+          uint4* sy = (uint4*)(smem + ml * CP + c8);
+          const uint4 yv = *sy;
+          const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+          const uint32_t yw[4] = {yv.x, yv.y, yv.z, yv.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            const uint32_t a = pack2(s0 * lo_f(xw[f]), s0 * hi_f(xw[f]));
+            uint32_t b = yw[f];
+            if constexpr (EPI == EPI_PE_B) b = pack2(s1 * lo_f(b), s1 * hi_f(b));
+            o[f] = pack2(lo_f(a) + lo_f(b), hi_f(a) + hi_f(b));
+          }
+          const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
+          *(uint4*)(ea.out + (size_t)(m0 + ml) * ea.ldo + n0 + c8) = ov;
+          if constexpr (EPI == EPI_PE_X) *sy = ov;
+        }
+        if constexpr (EPI == EPI_PE_X) {
+          if (ea.outT) {
+            __syncthreads();
+            // thread: column pair 2 cp, 2 cp + 1 and a band of BM / TB rows
+            constexpr int NP = BN / 2, TB = 256 / NP, RB = BM / TB;
+            const int cp = tid % NP, rb = tid / NP;
+#pragma unroll
+            for (int g = 0; g < RB / 8; ++g) {
+              const int r0 = rb * RB + 8 * g;
+              uint32_t w[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) w[e] = *(const uint32_t*)(smem + (r0 + e) * CP + 2 * cp);
+              uint4 c0, c1;
+              c0.x = (w[0] & 0xffffu) | (w[1] << 16); c0.y = (w[2] & 0xffffu) | (w[3] << 16);
+              c0.z = (w[4] & 0xffffu) | (w[5] << 16); c0.w = (w[6] & 0xffffu) | (w[7] << 16);
+              c1.x = (w[0] >> 16) | (w[1] & 0xffff0000u); c1.y = (w[2] >> 16) | (w[3] & 0xffff0000u);
+              c1.z = (w[4] >> 16) | (w[5] & 0xffff0000u); c1.w = (w[6] >> 16) | (w[7] & 0xffff0000u);
+              bf16_t* t0 = ea.outT + (size_t)(n0 + 2 * cp) * ea.ldoT + m0 + r0;
+              *(uint4*)t0 = c0;
+              *(uint4*)(t0 + ea.ldoT) = c1;
+            }
+          }
+        }
+        return;
+      }
+    }
     const bool vec = epi_vec_ok<EPI>(ea);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
