@@ -323,17 +323,18 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
   dim3 grid(nsplit, H, B + (pfon ? pf.slices : 0));
   const uint4* pfp = pfon ? (const uint4*)pf.p : nullptr;
   const size_t pfn = pfon ? pf.bytes / 16 : 0;
-  // more than two (b, h, split) work-groups per CU: the 128-VGPR form
-  static int cus = 0, force = -1;
+  // more than two (b, h, split) work-groups per CU: the three-waves-per-SIMD
+  // form (ANN_ATTN_RING=3 / 2 forces one; read at every call)
+  static int cus = 0;
   if (!cus) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    const char* e = getenv("ANN_ATTN_RING");
-    force = e ? atoi(e) : 0;
   }
+  const char* fe = getenv("ANN_ATTN_RING");
+  const int force = fe ? atoi(fe) : 0;
   const bool r2 = force == 2 || (force != 3 && (long long)nsplit * H * B > 2LL * cus);
 #define ANN_AD(D, R)                                                                         \
   hipLaunchKernelGGL((k_attn_dec<D, R>), grid, dim3(AD_THREADS), 0, st, qkv, kc, vc, pos, cs, sn, \

@@ -414,6 +414,44 @@ def test_decode_weight_prefetch_bitwise(monkeypatch):
     assert worst < LOGIT_TOL, worst
 
 
+def test_decode_attention_ring_forms_bitwise(monkeypatch):
+    """The decode attention has a three-chunk K/V ring (two work-groups per
+    CU) and a two-chunk one held to three waves per SIMD, taken by default when
+    the grid has more than two work-groups per CU.  Both walk each wave's key
+    chunks in the same order: logits are bitwise equal under either form, with
+    one and with two key splits, and within tolerance of the oracle."""
+    cfg = GPTConfig(vocab_size=704, num_layers=3, num_heads=2, model_dim=256, seq_len=48,
+                    window=8, long_layers=(2,))
+    p = perturb_lambdas(init_params(cfg, 51, dense=True))
+    B = 12
+    tok = np.random.default_rng(52).integers(0, cfg.vocab_size, (B, 30))
+
+    def run(ring, splits):
+        monkeypatch.setenv("ANN_ATTN_RING", str(ring))
+        monkeypatch.setenv("ANN_DEC_SPLITS", str(splits))
+        print(f"case attention ring {ring} splits {splits}", flush=True)
+        eng = _engine(cfg, p, B)
+        _, lg = eng.prefill(tok[:, :20], want_logits=True)
+        out = [lg.cpu()]
+        for i in range(20, 29):
+            _, lg = eng.decode(torch.from_numpy(tok[:, i].astype(np.int32)).cuda(),
+                               want_logits=True)
+            out.append(lg.cpu())
+        eng.check_device()
+        return torch.stack(out)
+
+    for splits in (1, 2):
+        r3, r2 = run(3, splits), run(2, splits)
+        assert torch.equal(r3, r2), splits
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    ref = [R.forward(prep, tok[:, :20], cache)[:, -1]]
+    for i in range(20, 29):
+        ref.append(R.forward(prep, tok[:, i:i + 1], cache)[:, -1])
+    worst = (r2 - torch.stack(ref)).abs().max().item()
+    assert worst < LOGIT_TOL, worst
+
+
 def test_wide_lm_head_64_row_tile():
     """A vocabulary wider than 8 d at 12 rows takes the large-tile MFMA GEMM
     with its 64-row work-group tile for the lm_head."""
