@@ -61,6 +61,10 @@ struct EpiArgs {
   // PE_X: transposed copy of the output, or null
   bf16_t* outT;
   int ldoT;
+  // batched STORE / PE_B with a symmetric M x M output (x x^T, b A + c A A):
+  // only the tiles on and above the diagonal are computed, each one above it
+  // also stored transposed at the mirrored position
+  int sym;
 };
 
 // Sampling parameters read by the sampler from device memory (so a captured

@@ -425,7 +425,9 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   static_assert((EPI != EPI_QKV && EPI != EPI_CE) || BN == GM_BN, "128-column tiles");
   // staged epilogues (QKV; PE_B / PE_X on full tiles) reuse the LDS for a bf16
   // BM x BN tile of row pitch BN + 8
-  constexpr bool STAGED = EPI == EPI_QKV || EPI == EPI_PE_B || EPI == EPI_PE_X;
+  // the batched plain store stages its 128 x 128 tiles for the symmetric form
+  constexpr bool STAGE_STORE = EPI == EPI_STORE && BM == GM_BM && BN == GM_BN && DEPTH == 1;
+  constexpr bool STAGED = EPI == EPI_QKV || EPI == EPI_PE_B || EPI == EPI_PE_X || STAGE_STORE;
   constexpr int SMEM = (BM + BN) * GM_BK > (STAGED ? BM * (BN + 8) : 0)
                            ? (BM + BN) * GM_BK
                            : BM * (BN + 8);
@@ -441,7 +443,17 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   // grid (correct under any dispatch order); batched launches keep the
   // identity.  Measured 3-6% faster per prefill GEMM.
   int tm = blockIdx.y, tn = blockIdx.x;
-  if (gridDim.z == 1) {
+  if (ea.sym) {
+    // symmetric output: blockIdx.x walks the tiles tn >= tm row by row
+    const int nb = (M + BM - 1) / BM;
+    int t = blockIdx.x;
+    tm = 0;
+    while (t >= nb - tm) {
+      t -= nb - tm;
+      ++tm;
+    }
+    tn = tm + t;
+  } else if (gridDim.z == 1) {
     const int nbn = gridDim.x, total = nbn * gridDim.y;
     const int bid = blockIdx.y * nbn + blockIdx.x;
     const int x = bid & 7, q = total >> 3, r = total & 7;
@@ -558,8 +570,55 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
       }
     }
   });
+  // tile^T of the staged bf16 tile (row pitch CP) to dst[(n0 + c) * ld + m0 + r]:
+  // a thread takes a column pair and a band of rows, 16-byte runs
+  auto store_transposed = [&](bf16_t* dst, int ld, auto cpc) __attribute__((always_inline)) {
+    constexpr int CP = decltype(cpc)::value;
+    constexpr int NP = BN / 2, TB = 256 / NP, RB = BM / TB;
+    const int cp = tid % NP, rb = tid / NP;
+#pragma unroll
+    for (int g = 0; g < RB / 8; ++g) {
+      const int r0 = rb * RB + 8 * g;
+      uint32_t w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = *(const uint32_t*)(smem + (r0 + e) * CP + 2 * cp);
+      uint4 c0, c1;
+      c0.x = (w[0] & 0xffffu) | (w[1] << 16); c0.y = (w[2] & 0xffffu) | (w[3] << 16);
+      c0.z = (w[4] & 0xffffu) | (w[5] << 16); c0.w = (w[6] & 0xffffu) | (w[7] << 16);
+      c1.x = (w[0] >> 16) | (w[1] & 0xffff0000u); c1.y = (w[2] >> 16) | (w[3] & 0xffff0000u);
+      c1.z = (w[4] >> 16) | (w[5] & 0xffff0000u); c1.w = (w[6] >> 16) | (w[7] & 0xffff0000u);
+      bf16_t* t0 = dst + (size_t)(n0 + 2 * cp) * ld + m0 + r0;
+      *(uint4*)t0 = c0;
+      *(uint4*)(t0 + ld) = c1;
+    }
+  };
   if constexpr (!SWAP) {
     // C layout of the 16x16 MFMA: lane holds column (lane & 15), rows 4 (lane >> 4) + r
+    if constexpr (STAGE_STORE) {
+      // symmetric form (full tiles, host-checked): staged bf16 tile, 16-byte
+      // row chunks, and the mirrored tile^T above the diagonal
+      if (ea.sym) {
+        constexpr int CP = BN + 8, CPR = BN / 8, NCH = BM * CPR / 256;
+        __syncthreads();   // every wave is done with the last K tile in LDS
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              smem[(wm * WM + i * 16 + (lane >> 4) * 4 + r) * CP + wn * WN + j * 16 + r16] =
+                  f2bf(acc[j][i][r]);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+          const int q = tid + 256 * u, ml = q / CPR, c8 = (q % CPR) * 8;
+          *(uint4*)(ea.out + (size_t)(m0 + ml) * ea.ldo + n0 + c8) =
+              *(const uint4*)(smem + ml * CP + c8);
+        }
+        if (tn != tm) store_transposed(ea.out, ea.ldo, std::integral_constant<int, CP>{});
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -678,30 +737,22 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
           }
           const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
           *(uint4*)(ea.out + (size_t)(m0 + ml) * ea.ldo + n0 + c8) = ov;
-          if constexpr (EPI == EPI_PE_X) *sy = ov;
+          *sy = ov;   // kept for a transposed copy
         }
+        // PE_X: the transposed copy x'^T; PE_B in the symmetric form: the
+        // mirrored tile above the diagonal
+        bf16_t* tdst = nullptr;
+        int tld = 0;
         if constexpr (EPI == EPI_PE_X) {
-          if (ea.outT) {
-            __syncthreads();
-            // thread: column pair 2 cp, 2 cp + 1 and a band of BM / TB rows
-            constexpr int NP = BN / 2, TB = 256 / NP, RB = BM / TB;
-            const int cp = tid % NP, rb = tid / NP;
-#pragma unroll
-            for (int g = 0; g < RB / 8; ++g) {
-              const int r0 = rb * RB + 8 * g;
-              uint32_t w[8];
-#pragma unroll
-              for (int e = 0; e < 8; ++e) w[e] = *(const uint32_t*)(smem + (r0 + e) * CP + 2 * cp);
-              uint4 c0, c1;
-              c0.x = (w[0] & 0xffffu) | (w[1] << 16); c0.y = (w[2] & 0xffffu) | (w[3] << 16);
-              c0.z = (w[4] & 0xffffu) | (w[5] << 16); c0.w = (w[6] & 0xffffu) | (w[7] << 16);
-              c1.x = (w[0] >> 16) | (w[1] & 0xffff0000u); c1.y = (w[2] >> 16) | (w[3] & 0xffff0000u);
-              c1.z = (w[4] >> 16) | (w[5] & 0xffff0000u); c1.w = (w[6] >> 16) | (w[7] & 0xffff0000u);
-              bf16_t* t0 = ea.outT + (size_t)(n0 + 2 * cp) * ea.ldoT + m0 + r0;
-              *(uint4*)t0 = c0;
-              *(uint4*)(t0 + ea.ldoT) = c1;
-            }
-          }
+          tdst = ea.outT;
+          tld = ea.ldoT;
+        } else if (ea.sym && tn != tm) {
+          tdst = ea.out;
+          tld = ea.ldo;
+        }
+        if (tdst) {
+          __syncthreads();
+          store_transposed(tdst, tld, std::integral_constant<int, CP>{});
         }
         return;
       }
@@ -1212,13 +1263,23 @@ hipError_t gemm_batched(int epi, const bf16_t* A, int lda, long long sA, const b
     return hipErrorInvalidValue;
   const int bm = M <= 64 ? 64 : GM_BM;
   dim3 grid((N + GM_BN - 1) / GM_BN, (M + bm - 1) / bm, batch);
+  EpiArgs e2 = ea;
+  // symmetric form: square outputs of whole 128 x 128 tiles, 16-byte aligned
+  e2.sym = ea.sym && (epi == EPI_STORE || epi == EPI_PE_B) && M == N && bm == GM_BM &&
+           M % GM_BM == 0 && ea.ldo % 8 == 0 && ((uintptr_t)ea.out & 15) == 0 &&
+           sOut % 8 == 0 && (epi != EPI_PE_B || (ea.ldr % 8 == 0 && sX % 8 == 0 &&
+                                                 ((uintptr_t)ea.x & 15) == 0));
+  if (e2.sym) {
+    const int nb = M / GM_BM;
+    grid = dim3(nb * (nb + 1) / 2, 1, batch);
+  }
 #define ANN_GB(E)                                                                              \
   if (bm == 64)                                                                                \
     hipLaunchKernelGGL((k_gemm_bat<E, 64>), grid, dim3(256), 0, st, A, lda, sA, W, sW, M, N,   \
-                       K, ea, sOut, sX);                                                       \
+                       K, e2, sOut, sX);                                                       \
   else                                                                                         \
     hipLaunchKernelGGL((k_gemm_bat<E, GM_BM>), grid, dim3(256), 0, st, A, lda, sA, W, sW, M,   \
-                       N, K, ea, sOut, sX);                                                    \
+                       N, K, e2, sOut, sX);                                                    \
   break;
   switch (epi) {
     case EPI_STORE: ANN_GB(EPI_STORE)

@@ -226,9 +226,11 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
     EpiArgs ea{};
     hipError_t e;
     if (!tall) {
-      // A = x x^T (M x M, K = N)
+      // A = x x^T (M x M, K = N); A and B below are symmetric: only the tiles
+      // on and above the diagonal are computed (their mirrors stored transposed)
       ea.out = am;
       ea.ldo = M;
+      ea.sym = 1;
       e = gemm_batched(EPI_STORE, cur, N, (long long)mn, cur, (long long)mn, M, M, N, ea,
                        (long long)S * S, 0, batch, st);
       if (e != hipSuccess) return e;
@@ -242,6 +244,7 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
                        (long long)S * S, (long long)S * S, batch, st);
       if (e != hipSuccess) return e;
       // x' = a x + B x: B (M x M) against x^T (N x M)
+      ea.sym = 0;
       ea.out = nxt;
       ea.ldo = N;
       ea.x = cur;
@@ -253,9 +256,10 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
                        (long long)mn, (long long)mn, batch, st);
       if (e != hipSuccess) return e;
     } else {
-      // A = x^T x (N x N, K = M) from x^T (N x M)
+      // A = x^T x (N x N, K = M) from x^T (N x M); A and B symmetric as above
       ea.out = am;
       ea.ldo = N;
+      ea.sym = 1;
       e = gemm_batched(EPI_STORE, xt, M, (long long)mn, xt, (long long)mn, N, N, M, ea,
                        (long long)S * S, 0, batch, st);
       if (e != hipSuccess) return e;
@@ -267,6 +271,7 @@ hipError_t polar_express(const float* g, int batch, int M, int N, bf16_t* out, v
       e = gemm_batched(EPI_PE_B, am, N, (long long)S * S, am, (long long)S * S, N, N, N, ea,
                        (long long)S * S, (long long)S * S, batch, st);
       if (e != hipSuccess) return e;
+      ea.sym = 0;
       // x' = a x + x B (B symmetric: its rows are the columns of B)
       ea.out = nxt;
       ea.ldo = N;
