@@ -78,6 +78,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+// Softcap with the hardware exp2 and reciprocal (a few fp32 ulps from the IEEE
+// form): the sampler's weights (its threshold comparisons use the IEEE form)
+// and the training loss's sums; the fp32 logits handed out use softcap().
+__device__ __forceinline__ float softcap_fast(float z) {
+  const float e = __builtin_amdgcn_exp2f((z + 5.0f) * -0.19235933878519512f);  // -log2(e) / 7.5
+  return 23.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
 // Softcap of the logits: 23 * sigmoid((z + 5) / 7.5).
 __device__ __forceinline__ float softcap(float z) {
   float t = (z + 5.0f) / 7.5f;

@@ -34,12 +34,6 @@ __device__ __forceinline__ float key2f(uint32_t k) {
   const uint32_t h = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
   return __uint_as_float(h << 16);
 }
-// Softcap with the hardware exp2 and reciprocal (weights only; the threshold
-// comparisons use the IEEE softcap).
-__device__ __forceinline__ float softcap_fast(float z) {
-  const float e = __builtin_amdgcn_exp2f((z + 5.0f) * -0.19235933878519512f);  // -log2(e) / 7.5
-  return 23.0f * __builtin_amdgcn_rcpf(1.0f + e);
-}
 // Number of packed 16-bit keys >= t (t >= 1): sat(key - (t - 1)) > 0.
 __device__ __forceinline__ uint32_t count_ge(const uint32_t* kk, uint32_t t) {
   const unsigned short t1 = (unsigned short)(t - 1);
