@@ -293,17 +293,35 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
   }
 }
 
-// Whether the projection routing (gemm()) sends (epi, M, N, K) here.  In the
+static int big_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+// Whether the projection routing (gemm()) sends (epi, M, N) here.  In the
 // 64 x 512-token prefill, per layer against the two-work-groups-per-CU tiles
 // of k_gemm_2w (rocprof, one box): fc (relu^2) 185 us here; o-proj (attention
 // residual) 79 us here with 192-column tiles (103 with 256, 108 in k_gemm_2w);
 // proj (MLP residual) 159 us here with 192-column tiles against 199 in
-// k_gemm_2w; qkv 173 us here against 155 in k_gemm_2w -- its QK-norm / RoPE /
-// cache-write epilogue is not overlapped by another work-group's MFMAs at one
-// work-group per CU.  The kernel still serves every epilogue of gemm_big()
-// when called directly.
-bool gemm_big_routes(int epi) {
-  return epi == EPI_RELU2 || epi == EPI_RESID_ATTN || epi == EPI_RESID_MLP;
+// k_gemm_2w.  QKV: 165 us here against 150 in k_gemm_2w at 64 x 512 tokens,
+// whose 1152 tiles leave the fifth round of 256 CUs half empty; with whole
+// rounds it wins (16 x 7680 tokens: 4320 tiles, 565 -> 535 us; d 1536 at
+// 128 x 1024: 9216 tiles, 2072 -> 1816 us), so QKV comes here when the last
+// round's idle CUs are under 5% of all rounds.  The kernel still serves every
+// epilogue of gemm_big() when called directly.
+bool gemm_big_routes(int epi, int M, int N) {
+  if (epi == EPI_RELU2 || epi == EPI_RESID_ATTN || epi == EPI_RESID_MLP) return true;
+  if (epi != EPI_QKV || N % BG_BN) return false;
+  const long long cus = big_cus(), tiles = (long long)((M + BG_BM - 1) / BG_BM) * (N / BG_BN);
+  const long long slots = (tiles + cus - 1) / cus * cus;
+  return (slots - tiles) * 20 < slots;
 }
 
 // Tile width for an M x N output: 256 or 192 columns, whichever needs fewer
@@ -316,16 +334,12 @@ bool gemm_big_routes(int epi) {
 // ANN_GEMM_BIG_BN=256 / 192 forces one where it divides N (read once per
 // process).
 static int big_bn(int epi, int M, int N) {
-  static int cus = 0, force = -1;
+  static int force = -1;
   if (force < 0) {
     const char* e = getenv("ANN_GEMM_BIG_BN");
     force = e ? atoi(e) : 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
   }
+  const int cus = big_cus();
   const bool ok192 = epi != EPI_QKV && N % 192 == 0, ok256 = N % 256 == 0;
   if (!ok192) return 256;
   if (!ok256) return 192;

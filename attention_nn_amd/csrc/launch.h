@@ -110,7 +110,7 @@ bool gemm_qkv_fits(int M, int N, int K, const EpiArgs& ea);
 // whether a shape can go there, gemm_big_routes which epilogues gemm() sends
 // there by itself (those measured faster than the k_gemm_2w tiles).
 bool gemm_big_fits(int epi, const bf16_t* A, int lda, int M, int N, int K, const EpiArgs& ea);
-bool gemm_big_routes(int epi);
+bool gemm_big_routes(int epi, int M, int N);
 hipError_t gemm_big(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N, int K,
                     const EpiArgs& ea, hipStream_t st);
 hipError_t gemm_batched(int epi, const bf16_t* A, int lda, long long sA, const bf16_t* W,

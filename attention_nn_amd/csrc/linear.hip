@@ -1338,7 +1338,7 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
   // there (read at every call)
   const char* big_env = getenv("ANN_GEMM_BIG");
   const int big_mode = big_env ? atoi(big_env) : 1;
-  if (big_mode != 0 && (big_mode == 2 || gemm_big_routes(epi)) &&
+  if (big_mode != 0 && (big_mode == 2 || gemm_big_routes(epi, M, N)) &&
       gemm_big_fits(epi, A, lda, M, N, K, ea)) {
     if (epi == EPI_QKV && !gemm_qkv_fits(M, N, K, ea)) return hipErrorInvalidValue;
     return gemm_big(epi, A, lda, W, M, N, K, ea, st);
