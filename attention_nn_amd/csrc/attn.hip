@@ -96,7 +96,7 @@ template <int DH, int BK, int NS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ap_waves_per_eu<DH, BK, NS>()))) void k_attn_prefill(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, bf16_t* __restrict__ out, int T, int H, int max_ctx,
-    int window, int is_long, float scale, float shift) {
+    int window, int is_long, float scale, float shift, int lpt) {
   constexpr int BQ = 128;
   constexpr int RB = DH * 2;          // LDS row bytes
   constexpr int TB = BK * RB;         // bytes of one K (or V) tile
@@ -109,17 +109,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ap_waves_pe
   constexpr int NI = BK / 32;         // 32-key steps of the PV product
   extern __shared__ __attribute__((aligned(16))) unsigned char ap_smem[];
 
-  // XCD-aware order: work-group L runs on XCD L % 8, so work item
-  // (L % 8) * N/8 + L / 8 puts consecutive items -- the query blocks of one
-  // (row, head), which read the same keys and values -- on one XCD and its L2
+  // Work order.  Work-group L runs on XCD L % 8.
+  //  * lpt (host: the NP (row, head) pairs of one query block fit the
+  //    resident work-groups): the query blocks of a sequence differ up to
+  //    nx-fold in key tiles, so the longest go first (work-group L takes
+  //    query block nx - 1 - L / NP of pair L % NP) and the short ones fill
+  //    the slots the long ones leave; with NP a multiple of 8 every block of
+  //    a pair lands on one XCD.  64 x 512 tokens: 81 -> 65 us per layer
+  //    (dispatched by pair it took 78 us for ~41 us of work per slot);
+  //    16 x 7680: 656 -> 620 us.
+  //  * otherwise (cfg5: 1536 pairs, three rounds per block): work item
+  //    (L % 8) * N/8 + L / 8 -- consecutive items, the query blocks of one
+  //    pair, run together on one XCD and share its L2 (longest-first measured
+  //    672 -> 707 us there: a pair's blocks rounds apart re-read its keys).
   int qb, h, b;
   {
-    const int nx = gridDim.x, ny = gridDim.y, N = nx * ny * gridDim.z;
+    const int nx = gridDim.x, ny = gridDim.y, NP = ny * gridDim.z, N = nx * NP;
     const int L = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
-    const int w = (N % 8 == 0) ? (L % 8) * (N / 8) + L / 8 : L;
-    qb = w % nx;
-    h = (w / nx) % ny;
-    b = w / (nx * ny);
+    if (lpt) {
+      qb = nx - 1 - L / NP;
+      h = (L % NP) % ny;
+      b = (L % NP) / ny;
+    } else {
+      const int w = (N % 8 == 0) ? (L % 8) * (N / 8) + L / 8 : L;
+      qb = w % nx;
+      h = (w / nx) % ny;
+      b = w / (nx * ny);
+    }
   }
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
@@ -316,8 +332,21 @@ static hipError_t attn_prefill_launch(dim3 grid, hipStream_t st, const bf16_t* q
   static hipError_t attr = hipFuncSetAttribute((const void*)k_attn_prefill<DH, BK, NS>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
+  // longest query blocks first when one block's (row, head) pairs fit the
+  // resident work-groups (ap_waves_per_eu: 4 waves per SIMD = two 8-wave
+  // work-groups per CU, else one)
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  const long long resident = (long long)cus * (ap_waves_per_eu<DH, BK, NS>() / 2);
+  const int lpt = (long long)grid.y * grid.z <= resident ? 1 : 0;
   hipLaunchKernelGGL((k_attn_prefill<DH, BK, NS>), grid, dim3(512), lds, st, q, kc, vc, pos, out, T,
-                     H, max_ctx, window, (int)long_layer, scale, shift);
+                     H, max_ctx, window, (int)long_layer, scale, shift, lpt);
   return hipGetLastError();
 }
 
