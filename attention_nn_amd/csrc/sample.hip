@@ -9,11 +9,16 @@
 //     running sum of exp(zc - max) exceeds u * total.
 // One work-group of 1024 threads per row; thread t holds the ordered 16-bit
 // keys of entries [56 t, 56 t + 56) in registers, two per dword.  The k-th
-// largest key comes from a binary search (count of keys >= T per round over
-// the packed keys, saturating 16-bit arithmetic) on [lb, kmax], where lb, the
-// k-th largest of the per-thread maxima, bounds it from below (k <= 1024).
-// The weights use the hardware exp2 / reciprocal; only chunks holding a kept
-// entry in some lane of the wave evaluate them.
+// largest of the per-thread maxima, lb, bounds the k-th largest key from
+// below (k <= the threads holding entries); wave 0 finds it by bisection over
+// the maxima, 16 per lane, with wave reductions only.  Every key >= lb (at
+// least k of them, and every kept one) is then copied to an LDS list, and if
+// the list holds at most 1024 keys wave 0 bisects over it the same way for
+// the k-th largest key.  A longer list (ties, flat logits, large k) falls
+// back to a bisection over all keys with block-wide counts per round (packed
+// saturating 16-bit arithmetic).  The weights use the hardware exp2 /
+// reciprocal; only chunks holding a kept entry in some lane of the wave
+// evaluate them.
 #include <math.h>
 #include "common.h"
 #include "launch.h"
@@ -23,6 +28,7 @@ namespace ann {
 constexpr int SMP_THREADS = 1024;
 constexpr int SMP_CH = 7;              // 16-byte chunks (8 entries) per thread
 constexpr int SMP_PER = SMP_CH * 8;    // entries per thread: Vs <= 57344
+constexpr int SMP_CAP = 1024;          // candidate list: 16 keys per lane of one wave
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Two bf16 values of a dword -> their order-preserving 16-bit keys
@@ -87,6 +93,27 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   return b;
 }
 
+// Largest T in [lo, hi] with at least k of the wave's keys >= T (16 per lane
+// as 8 packed pairs, 0 = no key; lo must satisfy it).  lo, hi and the counts
+// are wave-uniform; every T tried is >= 1.
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&v)[8], uint32_t lo, uint32_t hi,
+                                             uint32_t k) {
+  const u16x2 one = {1, 1};
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    const unsigned short t1 = (unsigned short)(mid - 1);
+    const u16x2 tm = {t1, t1};
+    u16x2 acc = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc += __builtin_elementwise_min(
+          __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, v[j]), tm), one);
+    if ((uint32_t)__ockl_wfred_add_i32((int)((uint32_t)acc.x + (uint32_t)acc.y)) >= k) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
 // Block sum of per-wave counts (wc uniform within each wave); buf alternates
 // between calls so that one barrier per call suffices.
 __device__ __forceinline__ uint32_t block_sum_waves(uint32_t wc, uint32_t* buf) {
@@ -108,10 +135,16 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   __shared__ uint32_t s_mm[2][SMP_THREADS / 64];
   __shared__ float s_wsum[SMP_THREADS / 64];
   __shared__ uint32_t s_misc[2];
+  __shared__ __attribute__((aligned(16))) unsigned short s_lmax[SMP_THREADS];
+  __shared__ __attribute__((aligned(16))) unsigned short s_list[SMP_CAP];
+  __shared__ uint32_t s_sel[2];   // [0] bound / threshold broadcast, [1] list length
   const float temperature = sp->temperature;
   const int top_k = sp->top_k;
   const uint64_t seed = sp->seed;
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // this row's position and step, read now rather than behind the last barrier
+  const int32_t pos0 = pos ? pos[row] : 0;
+  const uint64_t step = steps[row];
   const bf16_t* z = zall + (size_t)row * ldz;
   const int base = tid * SMP_PER;
   const int nvalid = max(0, min(SMP_PER, Vs - base));
@@ -148,7 +181,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     best = block_max_u64(best, s_red);
     if (tid == 0) {
       out_tok[row] = (int32_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-      if (pos) pos[row] += pos_adv;
+      if (pos) pos[row] = pos0 + pos_adv;
     }
     return;
   }
@@ -161,6 +194,8 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
       s_mm[0][wv] = wmax;
       s_mm[1][wv] = wmin;
     }
+    s_lmax[tid] = (unsigned short)lmax;
+    if (tid == 0) s_sel[1] = 0u;
   }
   __syncthreads();
   uint32_t kmax = 0, lmin = 0xffffffffu;
@@ -176,28 +211,73 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   const bool use_thr = top_k > 0 && top_k < Vs;
   if (use_thr) {
     uint32_t lo = 0, hi = kmax;
-    int round = 0;
+    bool found = false;
     if (top_k <= holders) {
       // lower bound: the top_k-th largest per-thread maximum (top_k threads
-      // each hold a key >= it), searched above the smallest maximum
-      uint32_t a = lmin, b = kmax;
-      while (a < b) {
-        const uint32_t mid = (a + b + 1) >> 1;
-        const uint32_t c = (uint32_t)__popcll(__ballot(lmax >= mid));
-        const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
-        if (tot >= (uint32_t)top_k) a = mid;
-        else b = mid - 1;
+      // each hold a key >= it), searched above the smallest maximum, which
+      // every holder reaches (threads without entries have maximum 0)
+      if (wv == 0) {
+        uint32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = ((const uint32_t*)s_lmax)[j * 64 + lane];
+        const uint32_t lb = wave_kth(v, lmin, kmax, (uint32_t)top_k);
+        if (lane == 0) s_sel[0] = lb;
       }
-      lo = a;
+      __syncthreads();
+      lo = s_sel[0];
+      if (lo > 0u) {
+        // candidates: every key >= lo, placed by a wave scan of the counts
+        const uint32_t cnt = count_ge(kk, lo);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t v = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += v;
+        }
+        uint32_t wb = 0;
+        if (lane == 63) wb = atomicAdd(&s_sel[1], incl);
+        wb = __shfl(wb, 63, 64);
+        if (cnt) {
+          uint32_t p = wb + incl - cnt;
+#pragma unroll
+          for (int j = 0; j < SMP_PER / 2; ++j) {
+            const uint32_t a = kk[j] & 0xffffu, b = kk[j] >> 16;
+            if (a >= lo) { if (p < (uint32_t)SMP_CAP) s_list[p] = (unsigned short)a; ++p; }
+            if (b >= lo) { if (p < (uint32_t)SMP_CAP) s_list[p] = (unsigned short)b; ++p; }
+          }
+        }
+        __syncthreads();
+        const uint32_t n = s_sel[1];   // >= top_k
+        if (n <= (uint32_t)SMP_CAP) {
+          // every key >= the k-th largest is listed: the list's k-th largest
+          if (wv == 0) {
+            uint32_t v[8];   // list entries 2i, 2i + 1; entries >= n read as 0
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t i = (uint32_t)(j * 64 + lane);
+              const uint32_t w = ((const uint32_t*)s_list)[i];
+              v[j] = (2 * i < n ? (w & 0xffffu) : 0u) | (2 * i + 1 < n ? (w & 0xffff0000u) : 0u);
+            }
+            const uint32_t t = wave_kth(v, lo, hi, (uint32_t)top_k);
+            if (lane == 0) s_sel[0] = t;
+          }
+          __syncthreads();
+          thr_key = s_sel[0];
+          found = true;
+        }
+      }
     }
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi + 1) >> 1;
-      const uint32_t c = (uint32_t)__ockl_wfred_add_i32((int)count_ge(kk, mid));
-      const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
-      if (tot >= (uint32_t)top_k) lo = mid;
-      else hi = mid - 1;
+    if (!found) {
+      int round = 0;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        const uint32_t c = (uint32_t)__ockl_wfred_add_i32((int)count_ge(kk, mid));
+        const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
+        if (tot >= (uint32_t)top_k) lo = mid;
+        else hi = mid - 1;
+      }
+      thr_key = lo;
     }
-    thr_key = lo;
   }
 
   // ---- kept set = keys >= tk.  softcap / temperature is non-decreasing in
@@ -261,7 +341,6 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     total += s_wsum[w];
   }
   const float before = wbase + incl - local;
-  const uint64_t step = steps[row];
   const uint32_t rw = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
                                (uint32_t)seed, (uint32_t)(seed >> 32));
   const float target = (float)(rw >> 8) * (1.0f / 16777216.0f) * total;
@@ -292,7 +371,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
     // rounding can leave the target at/after every interval: last kept entry
     const uint32_t pick = s_misc[0] != 0xffffffffu ? s_misc[0] : s_misc[1];
     out_tok[row] = (int32_t)pick;
-    if (pos) pos[row] += pos_adv;
+    if (pos) pos[row] = pos0 + pos_adv;
     steps[row] = step + 1;
   }
 }

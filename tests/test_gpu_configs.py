@@ -93,6 +93,67 @@ def test_cfg3_shape_b64_prefill512_topk50():
     assert draws == 64 * 4
 
 
+@pytest.mark.parametrize("case", ["period600", "levels"])
+def test_sampler_tied_logits_full_vocab(case):
+    """The top-k sampler over the real vocabulary with tied logits (k = 50,
+    T = 0.8).  period600: lm_head columns repeat with period 600, so each
+    logit value has ~84 copies, at most one per thread's 56 entries; the top
+    value's copies are all kept and fill the candidate list.  levels: every
+    column is one of three multiples of one vector (30, 2000 and the rest of
+    the columns), so 2030 or ~48,000 keys reach the per-thread-maxima bound
+    and the sampler falls back to its block-wide bisection from that bound.
+    Draws against the oracle sampler on the engine's own logits."""
+    cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 61, dense=True))
+    V = cfg.vocab_size
+    h = p["lm_head"]
+    if case == "period600":
+        p["lm_head"] = np.ascontiguousarray(h[:, np.arange(V) % 600] * 40)
+    else:
+        level = np.full(V, 2)
+        perm = np.random.default_rng(5).permutation(V)
+        level[perm[:30]], level[perm[30:2030]] = 0, 1
+        alpha = np.array([3.0, 2.0, 1.0], dtype=np.float32)
+        p["lm_head"] = np.ascontiguousarray(h[:, :1] * 40 * alpha[level][None, :])
+    print(f"case sampler ties {case}: d256 L2 V50304 B=8, T=0.8 top-k 50", flush=True)
+    B, T0, temp, k, seed = 8, 16, 0.8, 50, 99
+    tok = np.random.default_rng(7).integers(0, 50257, (B, T0 + 3))
+    eng = _engine(cfg, p, B, 64, B * T0)
+    nxt, lg = eng.prefill(tok[:, :T0], temp, k, seed=seed, step=0, want_logits=True)
+    edge = 0
+    for step in range(3):
+        if step:
+            t = torch.from_numpy(tok[:, T0 + step - 1].astype(np.int32)).cuda()
+            nxt, lg = eng.decode(t, temp, k, seed=seed, step=step, want_logits=True)
+        z, got = lg.cpu().numpy(), nxt.cpu().numpy()
+        for b in range(B):
+            r = _draw_position(int(got[b]), z[b, :50257], temp, k, S.uniform(seed, step, b))
+            assert r is not None, (case, step, b)
+            edge += r
+    eng.check_device()
+    # with ~48,000 tied maxima u * total keeps ~8 fraction bits in fp32
+    assert edge <= 2, edge
+
+
+def _draw_position(got, z, temp, k, u):
+    """0 if `got` is the oracle's draw; 1 if it is the neighbouring kept entry
+    across a cumulative boundary within 1e-5 of the total from u * total (the
+    device sums fp32 weights and forms u * total in fp32); None otherwise."""
+    zt = z.astype(np.float32) / np.float32(temp)
+    kth = np.sort(zt)[-k]
+    keep = np.nonzero(zt >= kth)[0]
+    c = np.cumsum(np.exp(zt[keep].astype(np.float64) - zt[keep].max()))
+    t = u * c[-1]
+    i = min(int(np.searchsorted(c, t, side="right")), keep.size - 1)
+    if keep[i] == got:
+        return 0
+    j = int(np.searchsorted(keep, got))
+    if j >= keep.size or keep[j] != got or abs(j - i) != 1:
+        return None
+    return 1 if abs(c[min(i, j)] - t) <= 1e-5 * c[-1] else None
+
+
 def test_cfg4_shape_ctx8192_b16():
     """cfg4's shapes: the 155M dims at max_ctx 8192, 16 sequences, a
     7680-token prefill (15 query blocks of 512; the windowed layers read 896
