@@ -384,7 +384,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the decode path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+              "(multi-GPU sharding is a design note, not built)", file=sys.stderr)
         return 2
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
