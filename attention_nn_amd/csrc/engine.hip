@@ -175,7 +175,7 @@ struct ann_ctx {
   int len = 0;  // tokens held per sequence
   int B = 0;    // sequences held
   // decode-step graph (captured once per key, replayed every step)
-  bool use_graph = true;
+  int graph_mode = -1;   // ANN_DECODE_GRAPH: 0 never, 1 always, unset: below GRAPH_MAX_B rows
   hipStream_t cap_st = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -321,6 +321,8 @@ int prefetch_wgs(ann_ctx* c, int B, size_t bytes) {
 }
 
 // embed + all layers for M = B*T rows whose positions start at pos[b].
+constexpr int GRAPH_MAX_B = 16;
+
 int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
   const ann_config& g = c->c;
   const int M = B * T, d = g.d, H = g.H, Dh = c->Dh;
@@ -662,7 +664,7 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->wl = weight_layout(*cfg);
   c->sl = ws_layout(*cfg);
   const char* ge = getenv("ANN_DECODE_GRAPH");
-  c->use_graph = !(ge && ge[0] == '0');
+  c->graph_mode = ge ? (ge[0] == '0' ? 0 : 1) : -1;
   const char* pe = getenv("ANN_PERSIST");
   c->pd_env = !(pe && pe[0] == '0');
   const char* on = getenv("ANN_PD_ON");
@@ -919,8 +921,12 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   // The batch-1 persistent step is one kernel (plus the sampler when not
   // greedy): launched directly, measured 2.5% more tokens per second than
   // replaying it as a graph (0.2019 against 0.2070 ms per token at 155M).
-  // The per-kernel path (tens of launches) replays its captured graph.
-  if (c->use_graph && c->prof_kind < 0 && !persist_ok(c, B))
+  // The per-kernel path (tens of launches) replays its captured graph below
+  // GRAPH_MAX_B rows; from there launched directly, ~4 us per step faster
+  // (batch 64 557.4 -> 553.0 us, 16 x 8192 504.1 -> 500.1, 128 rows equal),
+  // the host enqueueing a step well inside its GPU time.
+  const bool graph = c->graph_mode == 1 || (c->graph_mode < 0 && B < GRAPH_MAX_B);
+  if (graph && c->prof_kind < 0 && !persist_ok(c, B))
     rc = decode_graph(c, tokens, B, greedy, out_tok, logits, st);
   else
     rc = enqueue_decode(c, tokens, B, greedy, out_tok, logits, st);

@@ -301,3 +301,35 @@ def test_sampling_state_greedy_after_sampled_and_more_rows():
     for i in range(3):
         nxt, lg = eng.decode(nxt, 0.9, 10, seed=4, step=7 + i, want_logits=True)
         _check_draws(nxt, lg, 0.9, 10, 4, 7 + i, cfg.vocab_size)
+
+
+def test_decode_graph_and_direct_launch_bitwise(monkeypatch):
+    """The per-kernel decode path at 16 rows, replayed as a captured graph
+    (ANN_DECODE_GRAPH=1), launched directly (=0, the default from 16 rows)
+    and with the default: the same tokens and bitwise-equal logits over
+    sampled steps (T = 0.8, top-k 50), so both launch forms stay covered."""
+    cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 71, dense=True))
+    B, T0, steps = 16, 24, 5
+    tok = np.random.default_rng(9).integers(0, 50257, (B, T0))
+    print("case decode launch forms: d256 L2 B=16, graph / direct / default", flush=True)
+    runs = {}
+    for mode in ("1", "0", None):
+        if mode is None:
+            monkeypatch.delenv("ANN_DECODE_GRAPH", raising=False)
+        else:
+            monkeypatch.setenv("ANN_DECODE_GRAPH", mode)
+        eng = _engine(cfg, p, B, 64, B * T0)
+        nxt, lg = eng.prefill(tok, 0.8, 50, seed=5, step=0, want_logits=True)
+        toks, lgs = [nxt.cpu()], [lg.cpu()]
+        for i in range(steps):
+            nxt, lg = eng.decode(nxt, 0.8, 50, seed=5, step=i + 1, want_logits=True)
+            toks.append(nxt.cpu())
+            lgs.append(lg.cpu())
+        eng.check_device()
+        runs[mode] = (torch.stack(toks), torch.stack(lgs))
+        del eng
+    for mode in ("0", None):
+        assert torch.equal(runs[mode][0], runs["1"][0]), mode
+        assert torch.equal(runs[mode][1], runs["1"][1]), mode
