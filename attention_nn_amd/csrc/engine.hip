@@ -252,14 +252,14 @@ struct ProfScope {  // records an event pair around a launch of the profiled kin
 bool proj_is_gemm(int M, int N, int K, int pre) {
   // the skinny GEMM re-reads W per 16 rows and A per 16 columns: wide
   // outputs (lm_head) go to the large-tile GEMM
-  return !gemv_fits(M, K) && !(N <= 8 * K && gemm_skinny_fits(M, N, K, pre == PRE_RMS));
+  return !gemv_routes(M, K) && !(N <= 8 * K && gemm_skinny_fits(M, N, K, pre == PRE_RMS));
 }
 
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st) {
   // the QKV and CE epilogues exist on the MFMA GEMM only
   const bool gemm_only = epi == EPI_CE;
-  const bool use_gemv = !gemm_only && gemv_fits(M, K);
+  const bool use_gemv = !gemm_only && gemv_routes(M, K);
   const bool use_sk = !gemm_only && !use_gemv && !proj_is_gemm(M, N, K, pre);
   if (epi == EPI_QKV && (use_gemv || use_sk)) return fail(ANN_E_ARG, "fused QKV needs the MFMA GEMM");
   // 65-128 rows with an RMS prologue and a plain-store epilogue (qkv, fc):
@@ -450,7 +450,7 @@ int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, flo
   EpiArgs ez{};
   ez.logits = logits;
   ez.ldz = g.V;
-  const bool fused_greedy = greedy && gemv_fits(B, g.d);
+  const bool fused_greedy = greedy && gemv_routes(B, g.d);
   unsigned long long* keys = c->sp<unsigned long long>(c->sl.amax);
   if (fused_greedy) {
     ez.amax = keys;

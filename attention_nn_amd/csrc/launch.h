@@ -95,6 +95,7 @@ hipError_t qkv_post(const bf16_t* qkv, bf16_t* q, bf16_t* kc, bf16_t* vc, const 
 hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int M, int N, int K,
                 float eps, const EpiArgs& ea, hipStream_t st);
 bool gemv_fits(int M, int K);
+bool gemv_routes(int M, int K);   // the engine's choice: the rows the GEMV takes
 int gemv_blocks(int N, int K);
 hipError_t argmax_finalize(const unsigned long long* keys, int nkeys, int M, int32_t* out_tok,
                            int32_t* pos, int pos_adv, hipStream_t st);

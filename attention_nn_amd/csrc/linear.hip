@@ -325,6 +325,12 @@ bool gemv_fits(int M, int K) {
   return M >= 1 && M <= 8 && (size_t)M * K * 2 <= 64 * 1024 && K % 8 == 0;
 }
 
+// Projections the engine sends to the GEMV: one or two rows.  From four rows
+// the skinny MFMA GEMMs are faster (155M decode step, sampled: 4 rows 405.5
+// -> 338.2 us, 8 rows 607.3 -> 365.5 us; 2 rows 310.1 on the GEMV against
+// 315.1).
+bool gemv_routes(int M, int K) { return M <= 2 && gemv_fits(M, K); }
+
 // U = 16-byte weight chunks each lane keeps in flight: enough to hold the
 // whole row slice when K / (8 LPR) <= 8, without spilling for short rows.
 template <int M, int LPR, int EPI, int PRE>
