@@ -1178,9 +1178,14 @@ hipError_t gemm_skinny(int epi, bool rms, const bf16_t* A, int lda, const bf16_t
                        int K, float eps, const EpiArgs& ea, hipStream_t st) {
   if (!gemm_skinny_fits(M, N, K, rms) || lda % 8) return hipErrorInvalidValue;
   // 32x32 work-group tiles halve the L2 re-reads of A and W; 16x16 tiles give
-  // more work-groups.  Measured: 32x32 wins above 64 rows and for wide N at
-  // 33-64 rows, 16x16 for narrow N at 64 rows.
-  const int T = (M > 64 || (M > 32 && N >= 2048)) ? 2 : 1;
+  // more work-groups.  Measured: 32x32 wins for wide N at 33-64 rows, 16x16
+  // for narrow N at 64 rows; above 64 rows 32x32 wins where its grid still
+  // has 128 or more work-groups (d 1536 o / proj at 128 rows, 192: 2982
+  // against 3186 us per cfg5 step) and loses below (d 768 at 96 / 128 rows,
+  // 72 / 96 work-groups: 764.9 -> 708.8, 818.6 -> 764.2 us per step with
+  // 16x16).  The RMS projections above 64 rows keep 32x32.
+  const long long g2 = (long long)((N + 31) / 32) * ((M + 31) / 32);
+  const int T = (M > 64 ? (rms || g2 >= 128) : (M > 32 && N >= 2048)) ? 2 : 1;
   dim3 grid((N + 16 * T - 1) / (16 * T), (M + 16 * T - 1) / (16 * T));
   // batch depth: the wave's whole K quarter when it fits (fewer registers ->
   // more resident work-groups)

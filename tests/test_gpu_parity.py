@@ -332,7 +332,9 @@ def test_persistent_matches_kernel_path(monkeypatch):
 @pytest.mark.parametrize("B", [40, 80])
 def test_decode_wide_batch_skinny_tiles(B):
     """Decode at 40 and 80 rows: the skinny MFMA GEMM with 32x32 work-group
-    tiles (above 64 rows, and for N >= 2048 above 32 rows) against the oracle."""
+    tiles for N >= 2048 above 32 rows (fc at 40 rows) and with 16x16 tiles
+    above 64 rows where the 32x32 grid would hold under 128 work-groups (o /
+    proj at d = 512, 80 rows), against the oracle."""
     cfg = GPTConfig(vocab_size=600, num_layers=2, num_heads=4, model_dim=512, seq_len=32,
                     window=8, long_layers=(1,))
     p = perturb_lambdas(init_params(cfg, 41, dense=True))
@@ -352,10 +354,11 @@ def test_decode_wide_batch_skinny_tiles(B):
 
 def test_decode_deep_load_rings():
     """Decode at 72 rows of a d = 768 model: the qkv / fc projections on
-    64 x 64 MFMA tiles with four K tiles in flight, the proj projection
-    (K = 3072) on the LDS-staged skinny GEMM with three rounds in flight per
-    wave, and (vocabulary above 8 d) the lm_head on the 128-row MFMA tiles;
-    logits against the oracle."""
+    64 x 64 MFMA tiles with four K tiles in flight, the o / proj projections
+    (K = 768 / 3072) on the LDS-staged skinny GEMM with 16 x 16 tiles (a
+    32 x 32 grid would hold 72 work-groups), and (vocabulary above 8 d) the
+    lm_head on the 128-row MFMA tiles; logits against the oracle.  The 32 x 32
+    tiles with three rounds in flight run in the cfg5-shape test."""
     cfg = GPTConfig(vocab_size=8192, num_layers=2, num_heads=6, model_dim=768, seq_len=16,
                     window=8, long_layers=(1,))
     p = perturb_lambdas(init_params(cfg, 47, dense=True))
