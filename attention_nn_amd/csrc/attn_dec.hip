@@ -272,7 +272,7 @@ void k_attn_dec(
   // last ticket sums all of them in split order and writes o = O / L
   const unsigned ticket = s_ticket;
   const uint32_t tag = ticket / 64u + 1u;
-  u64* pbase = part + ((size_t)b * H + h) * nsplit * (DH + 1);
+  u64* pbase = part + ((size_t)b * H + h) * AD_MAX_SPLIT * (DH + 1);
   u64* pp = pbase + (size_t)split * (DH + 1);
   if (tid < DH) ll_store(pp + tid, __float_as_uint(ot), tag);
   if (tid == 0) ll_store(pp + DH, __float_as_uint(lt), tag);
@@ -316,7 +316,7 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
                        bf16_t* out,
                        int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
                        float eps, int nsplit, const WeightPrefetch& pf, hipStream_t st) {
-  if (nsplit < 1 || nsplit > 64 || B <= 0) return hipErrorInvalidValue;
+  if (nsplit < 1 || nsplit > AD_MAX_SPLIT || B <= 0) return hipErrorInvalidValue;
   const bool pfon = pf.slices > 0 && pf.bytes >= 16 && pf.p && pf.sink;
   if (pfon && ((uintptr_t)pf.p & 15)) return hipErrorInvalidValue;
   const float shift = scale * (float)Dh * 1.02f;

@@ -46,7 +46,7 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr size_t ALIGN = 256;
-constexpr int MAX_SPLIT = 32;
+constexpr int MAX_SPLIT = AD_MAX_SPLIT;
 
 size_t up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
 
@@ -199,7 +199,8 @@ struct ann_ctx {
   bool pd_env = true;    // ANN_PERSIST=0 disables
   bool pd_coop = false;  // ANN_PERSIST_COOP=1: cooperative launch
   // the persistent step's exchange area, the error word and the decode
-  // attention's ticket counters must be cleared before the next decode step
+  // attention's ticket counters and partials must be cleared before their
+  // next user (a decode step or a one-token forward; clear_decode_state)
   bool dec_clear = true;
   // decode (batch >= 16): prefetch work-groups per attention launch that read
   // the next projections' weights ahead; -1 = not read yet, -2 = sized by
@@ -320,12 +321,33 @@ int prefetch_wgs(ann_ctx* c, int B, size_t bytes) {
   return n < 32 ? 32 : n > 512 ? 512 : (int)n;
 }
 
+// Zero the decode state once after ann_bind, before the first launch that
+// uses it: the persistent step's exchange area (tags, generation, error word),
+// the decode attention's ticket counters and its split partials.  That first
+// launch is a decode step, or a forward of one token per sequence (its
+// attention is the decode kernel too).  Never inside a graph capture: a
+// captured decode step only follows a decode step that has cleared.
+int clear_decode_state(ann_ctx* c, hipStream_t st) {
+  if (!c->dec_clear) return ANN_OK;
+  const ann_config& g = c->c;
+  HIPCHK(hipMemsetAsync(c->ws + c->sl.pd, 0, c->sl.pd_bytes, st));
+  HIPCHK(hipMemsetAsync(c->ws + c->sl.acnt, 0, (size_t)g.max_batch * g.H * 4, st));
+  HIPCHK(hipMemsetAsync(c->ws + c->sl.part, 0,
+                        (size_t)g.max_batch * g.H * MAX_SPLIT * (c->Dh + 1) * 8, st));
+  c->dec_clear = false;
+  return ANN_OK;
+}
+
 // embed + all layers for M = B*T rows whose positions start at pos[b].
 constexpr int GRAPH_MAX_B = 16;
 
 int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
   const ann_config& g = c->c;
   const int M = B * T, d = g.d, H = g.H, Dh = c->Dh;
+  if (T == 1) {   // the decode attention's counters and partials start from zero
+    const int rc0 = clear_decode_state(c, st);
+    if (rc0) return rc0;
+  }
   bf16_t* x = c->sp<bf16_t>(c->sl.x);
   bf16_t* x0 = c->sp<bf16_t>(c->sl.x0);
   bf16_t* qkv = c->sp<bf16_t>(c->sl.qkv);
@@ -722,7 +744,7 @@ int ann_check_device(ann_ctx* c, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
-  if (c->dec_clear) return ANN_OK;   // no decode step has run since binding
+  if (c->dec_clear) return ANN_OK;   // no decode-state user has run since binding
   unsigned* err = (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8));
   unsigned h = 0;
   HIPCHK(hipMemcpy(&h, err, sizeof h, hipMemcpyDeviceToHost));
@@ -913,11 +935,8 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   rc = sync_sampling(c, s, B, st);
   if (rc) return rc;
   const bool greedy = s->temperature == 0.f;
-  if (c->dec_clear) {   // tags, tickets and the error word start from zero
-    HIPCHK(hipMemsetAsync(c->ws + c->sl.pd, 0, c->sl.pd_bytes, st));
-    HIPCHK(hipMemsetAsync(c->ws + c->sl.acnt, 0, (size_t)c->c.max_batch * c->c.H * 4, st));
-    c->dec_clear = false;
-  }
+  rc = clear_decode_state(c, st);   // tags, tickets, partials and the error word
+  if (rc) return rc;
   // The batch-1 persistent step is one kernel (plus the sampler when not
   // greedy): launched directly, measured 2.5% more tokens per second than
   // replaying it as a graph (0.2019 against 0.2070 ms per token at 155M).

@@ -180,7 +180,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
       constexpr int j = decltype(jc)::value;
       b1[j] = bg_lds_read<j * 16 * BG_BK * 2>(pb1);
     });
-    bg_wait_lgkm<NJ>();   // b0 and a; the b1 reads may still fly
+    // b0 and a; the b1 reads may still fly.  A wave's LDS reads return in
+    // issue order, so lgkmcnt(NJ) leaves only the last NJ issued (the b1
+    // reads) outstanding; any scalar load the compiler has in flight counts
+    // on the same counter and only makes the wait stricter.  The lgkmcnt(0)
+    // after each MFMA group covers the next A fragment the same way.
+    bg_wait_lgkm<NJ>();
     bg_static_for<0, 16>([&](auto gc) __attribute__((always_inline)) {
       constexpr int g = decltype(gc)::value;
       constexpr int i = g & 7, kh = g >> 3;
@@ -198,6 +203,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_big(const bf16_t* A, int lda, c
       if constexpr (g < 15) bg_wait_lgkm<0>();
       a = an;
     });
+    // After the loop the accumulators leave their AGPRs through
+    // v_accvgpr_read / _mov (the epilogue and the register allocator's
+    // copies).  The compiler's hazard recognizer does not see these MFMAs
+    // (inline assembly), so the wait states an XDL result needs before a VALU
+    // or v_accvgpr instruction reads it are placed here by hand: the CDNA3 /
+    // CDNA4 ISA's MAI dependency table asks NumPasses + 3 (+1 on gfx950) for
+    // "XDL write VGPR -> VALU read", 12 for the 8-pass
+    // v_mfma_f32_16x16x32_bf16; three s_nop 7 give 24.  In the loop body,
+    // after the last MFMA group, every copy on the loop's exit path comes
+    // after them; they issue while the MFMA pipe drains the group, before
+    // the barrier.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     __syncthreads();
   }
 

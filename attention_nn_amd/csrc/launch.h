@@ -163,6 +163,8 @@ hipError_t attn_prefill(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, con
 // of HBM.  slices = extra grid.z slices (each nsplit x H work-groups); 0 = none.
 // sink: one 8-byte word the reads are folded into (written only on a 64-bit
 // match with a fixed constant, so the loads cannot be optimised away).
+constexpr int AD_MAX_SPLIT = 32;   // key splits per (b, h) of the decode attention
+
 struct WeightPrefetch {
   const void* p = nullptr;   // 16-byte aligned
   size_t bytes = 0;
@@ -172,8 +174,11 @@ struct WeightPrefetch {
 
 // Decode attention with fused QK-norm / RoPE / KV append (one token per
 // sequence) -> out (B, H*Dh) bf16.  part: split scratch of tagged words
-// (B, H, nsplit, Dh + 1); cnt: B*H ticket counters, multiples of 64 between
-// calls (zero before the first); err: set if a bounded wait gave up.
+// (B, H, AD_MAX_SPLIT, Dh + 1) -- a fixed stride per (b, h), so a slot is only
+// ever written by the splits of its own (b, h), whose tags only grow, whatever
+// nsplit a launch uses; cnt: B*H ticket counters, multiples of 64 between
+// calls (zero before the first, with part zeroed too); err: set if a bounded
+// wait gave up.
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,
                        const float* cs, const float* sn, u64* part, unsigned* cnt, unsigned* err,
                        bf16_t* out,

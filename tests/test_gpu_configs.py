@@ -182,6 +182,23 @@ def test_cfg5_shape_d1536_b128_topk50():
     assert draws == 128 * 4
 
 
+def test_cfg5_full_prompts_d1536_b128_prefill1024_topk50():
+    """cfg5 at its own prompt length: d1536 H12 x 128 at the full vocabulary,
+    128 sequences of 1024-token prompts -- a 131,072-row prefill (QKV with its
+    fused epilogue on the 256 x 256 GEMM, two 512-query blocks per (row, head)
+    in the prefill attention) -- then decode steps at positions 1024..1026
+    (past the first 1024 keys on the full-causal layer) with T = 0.8, top-k
+    50.  Three layers, layer 1 full-causal; rows 0, 77 and 127 against the
+    oracle, every row's draw against the oracle sampler."""
+    cfg = GPTConfig(num_layers=3, num_heads=12, model_dim=1536, seq_len=1040, window=384,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 57, dense=True))
+    print("case cfg5 full prompts: d1536 L3 V50304 B=128 T0=1024, T=0.8 top-k 50", flush=True)
+    worst, draws = _run_case(cfg, p, 128, 1024, 4, [0, 77, 127], 0.8, 50, 7, 1040)
+    assert worst < LOGIT_TOL, worst
+    assert draws == 128 * 4
+
+
 def test_cfg1_degenerate_64_greedy_steps():
     """cfg1 as specified (76.7M, model.py init: Wo = proj = x0 = 0), 16-token
     prompt, all 64 greedy steps: every step repeats the last prompt token and

@@ -224,11 +224,13 @@ def test_forward_loss_equals_cross_entropy_of_own_logits():
     assert abs(mean.item() - ref.mean().item()) < 1e-5
 
 
-@pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 12)])
+@pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 4), ("dh128", 8),
+                                    ("dh128", 12)])
 def test_decode_teacher_forced_past_window(name, B):
     """Decode logits at every position (well past the window) match the
-    oracle's KV-cache forward on the same tokens (B=12 takes the skinny MFMA
-    GEMM and the split-combine kernel instead of the GEMV)."""
+    oracle's KV-cache forward on the same tokens (two rows take the GEMV with
+    the fused greedy keys; 4, 8 and 12 rows the skinny MFMA GEMMs, the logits
+    GEMM and the sampler kernel, and the split-combine attention)."""
     cfg = small_cfgs()[name]
     p = perturb_lambdas(init_params(cfg, 5, dense=True))
     T0, steps = 7, cfg.seq_len - 7
@@ -244,6 +246,62 @@ def test_decode_teacher_forced_past_window(name, B):
         _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
         ref = R.forward(prep, t[:, None], cache)[:, -1]
         worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    assert worst < LOGIT_TOL, worst
+
+
+@pytest.mark.parametrize("B", [4, 8])
+def test_decode_small_batch_sampled_matches_oracle(B):
+    """Sampled decode (T = 0.9, top-k 20) at 4 and 8 rows: the logits match
+    the oracle at every step and every row's draw equals the oracle sampler's
+    draw (Philox counter (step, row)) from the engine's own logits."""
+    cfg = small_cfgs()["dh128"]
+    p = perturb_lambdas(init_params(cfg, 25, dense=True))
+    T0, steps, temp, k, seed = 7, 30, 0.9, 20, 77
+    tok = np.random.default_rng(3 + B).integers(0, cfg.vocab_size, (B, T0 + steps))
+    eng = _engine(cfg, p, B)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    nxt, lg = eng.prefill(tok[:, :T0], temp, k, seed=seed, step=0, want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :T0], cache)[:, -1]).abs().max().item()
+    draws = [(nxt, lg, 0)]
+    for i in range(steps - 1):
+        t = tok[:, T0 + i]
+        nxt, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), temp, k, seed=seed,
+                             step=i + 1, want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+        draws.append((nxt, lg, i + 1))
+    eng.check_device()
+    assert worst < LOGIT_TOL, worst
+    for nxt, lg, step in draws:
+        got, z = nxt.cpu().numpy(), lg.cpu().numpy()
+        for b in range(B):
+            want = _sample_small(z[b, :min(50257, cfg.vocab_size)], temp, k, S.uniform(seed, step, b))
+            assert int(got[b]) == want, (step, b)
+
+
+def test_one_token_prompts_then_decode_match_oracle():
+    """Prompts of one token at 4 rows: the prefill's attention is then the
+    decode kernel itself, with 8 key splits on the full-causal layers (ticket
+    counters and tagged partials), so the decode steps after it continue from
+    the counters it left.  Logits match the oracle's KV-cache forward at every
+    step, and no bounded wait timed out."""
+    cfg = GPTConfig(vocab_size=1000, num_layers=3, num_heads=2, model_dim=256, seq_len=512,
+                    window=8, long_layers=(0, 2))
+    p = perturb_lambdas(init_params(cfg, 31, dense=True))
+    B, steps = 4, 24
+    tok = np.random.default_rng(31).integers(0, cfg.vocab_size, (B, 1 + steps))
+    eng = _engine(cfg, p, B, ctx=512, tokens=4 * B)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :1], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :1], cache)[:, -1]).abs().max().item()
+    for i in range(steps):
+        t = tok[:, 1 + i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
     assert worst < LOGIT_TOL, worst
 
 
@@ -542,6 +600,31 @@ def test_greedy_155m_identical_64_steps():
     worst = max((g - r).abs().max().item() for g, r in zip(glog[:n_same], rlog[:n_same]))
     assert worst < LOGIT_TOL, worst
     assert got == ref, f"first divergence at step {n_same}"
+
+
+def test_persistent_155m_late_positions_match_oracle():
+    """The 155M model at batch 1 near the end of cfg2's context: a 1000-token
+    prefill, then teacher-forced decode steps on the persistent kernel at
+    positions 1000..1022 -- the windowed layers read keys [p - 383, p] over
+    three 128-key splits with lo > 0, the full-causal layers all p + 1 keys
+    over eight.  Logits within 2e-2 of the oracle at every step."""
+    cfg = cfg_155m()
+    p = perturb_lambdas(init_params(cfg, 9, dense=True))
+    tok = np.random.default_rng(91).integers(0, 50257, (1, 1024))
+    eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    print("case 155M batch 1: prefill 1000, decode at positions 1000..1022", flush=True)
+    _, lg = eng.prefill(tok[:, :1000], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :1000], cache, last_only=True)[:, -1]).abs().max().item()
+    for i in range(1000, 1023):
+        t = tok[:, i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache, last_only=True)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
+    assert eng.length == 1023
+    assert worst < LOGIT_TOL, worst
 
 
 def test_degenerate_init_repeats_last_token():

@@ -289,3 +289,158 @@ def test_mix_order_is_below_resolution_but_documented(monkeypatch):
     _mix_order(monkeypatch)
     g = _gap(_oracle(p, tok), want)
     assert not _differs(g), g
+
+
+# ---- the composed q / k path: QK-norm, RoPE at each row's position, 0.1 scale ----
+#
+# One layer with fc = 0, so the MLP adds nothing and the output is fixed by
+# attention alone (model.py:242-256): q = rope(rms(q)), k = rope(rms(k)) at
+# each row's own position, scores 0.1 q.k over the causal keys, a plain
+# softmax, P.V.  The brute force below builds the RoPE tables and applies the
+# pair rotation with its own loop (the reference's known-answer loop,
+# metal_kernels.py:356-362: pairs (2 p, 2 p + 1) for p < D/4 take
+# y0 = c x0 + s x1, y1 = c x1 - s x0, the rest pass through) and computes the
+# softmax in fp64 -- nothing goes through the oracle's attention or RoPE.
+
+QK_CFG = GPTConfig(vocab_size=512, num_layers=1, num_heads=2, model_dim=128, seq_len=32,
+                   window=16, long_layers=(0,))
+
+
+def _qk_params(seed):
+    p = init_params(QK_CFG, seed, dense=True)
+    p["resid_lambdas"] = np.array([[0.5, 1.125]], np.float32)
+    p["post_lambdas"] = np.array([[1.5, 0.75]], np.float32)
+    p["x0_lambdas"] = np.array([0.25], np.float32)
+    p["sa_lambdas"] = np.array([[0.875, 1.25]], np.float32)
+    p["fc_bank"] = np.zeros_like(p["fc_bank"])
+    return p
+
+
+def _rope_pairs(x, t, base=1024.0):
+    """x (H, D) of the row at position t: the pair loop with its own tables."""
+    D = x.shape[-1]
+    d4 = D // 4
+    freqs = np.power(np.float32(1.0 / base), np.linspace(0.0, 1.0, d4, dtype=np.float32))
+    theta = (np.float32(t) * freqs).astype(np.float32)
+    c, s = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    y = x.astype(np.float32).copy()
+    for p2 in range(d4):
+        x0, x1 = x[:, 2 * p2].astype(np.float32), x[:, 2 * p2 + 1].astype(np.float32)
+        y[:, 2 * p2] = c[p2] * x0 + s[p2] * x1
+        y[:, 2 * p2 + 1] = c[p2] * x1 - s[p2] * x0
+    return bf(y)
+
+
+def closed_form_qk_path(p, tok):
+    """Brute force of one full-causal layer with fc = 0 (B, T tokens from
+    position 0): returns (rms(x_L), softcapped logits)."""
+    B, T = tok.shape
+    d, H = QK_CFG.model_dim, QK_CFG.num_heads
+    Dh = d // H
+    res, post, x0l, sal = (bf(p[k]) for k in ("resid_lambdas", "post_lambdas", "x0_lambdas",
+                                               "sa_lambdas"))
+    ab = p["attn_bank"][0]
+    wqkv = bf(np.concatenate([bf(ab[0]), bf(ab[1]), bf(ab[2])], -1) * sal[0, 0])
+    wo = bf(bf(ab[3]) * sal[0, 1])
+    x = _embed(p, tok)
+    x0 = x
+    qkv = mm_bf(rms_bf(x), wqkv).reshape(B, T, 3, H, Dh)
+    y = np.zeros((B, T, H, Dh), np.float32)
+    for b in range(B):
+        q = [_rope_pairs(rms_bf(qkv[b, t, 0]), t) for t in range(T)]
+        k = [_rope_pairs(rms_bf(qkv[b, t, 1]), t) for t in range(T)]
+        v = qkv[b, :, 2].astype(np.float64)
+        for i in range(T):
+            for h in range(H):
+                s = np.array([0.1 * np.dot(q[i][h].astype(np.float64), k[j][h].astype(np.float64))
+                              for j in range(i + 1)])
+                w = np.exp(s - s.max())
+                w /= w.sum()
+                y[b, i, h] = (w[:, None] * v[:i + 1, h]).sum(0)
+    o = mm_bf(bf(y).reshape(B, T, d), wo)
+    x = bf(bf(bf(res[0, 0] * x) + bf(post[0, 0] * o)) + bf(x0l[0] * x0))
+    x = bf(res[0, 1] * x)                      # + post * 0 adds nothing
+    return _head(p, x)
+
+
+def _qk_tokens(T):
+    return np.random.default_rng(29).integers(0, QK_CFG.vocab_size, (3, T))
+
+
+@pytest.mark.parametrize("T", [3, 12])
+def test_oracle_qk_path_equals_brute_force(T):
+    p = _qk_params(7)
+    tok = _qk_tokens(T)
+    g = _gap(_oracle(p, tok, QK_CFG), closed_form_qk_path(p, tok))
+    assert _matches(g), g
+
+
+def test_oracle_qk_path_decode_equals_brute_force():
+    """The same path through the oracle's KV cache: a 1-token prefill, then one
+    token per step, every row at its own position (q rotated at t, the cached
+    keys at theirs)."""
+    p = _qk_params(8)
+    tok = _qk_tokens(6)
+    want = closed_form_qk_path(p, tok)
+    prep = R.Prepared(QK_CFG, p)
+    cache = R.KVCache(1)
+    rows = [R.forward(prep, tok[:, i:i + 1], cache, return_hidden=True) for i in range(6)]
+    got = (torch.cat([r[2] for r in rows], 1).numpy(), torch.cat([r[0] for r in rows], 1).numpy())
+    assert _matches(_gap(got, want))
+
+
+def _plant_scale(monkeypatch):
+    f = R.attention
+    monkeypatch.setattr(R, "attention", lambda q, k, v, keep, scale, *a, **kw:
+                        f(q, k, v, keep, 1.0 / np.sqrt(q.shape[-1]), *a, **kw))
+
+
+def _plant_rope_q_only(monkeypatch):
+    f, calls = R.rope_ht, [0]
+
+    def g(x, cs, sn, pos):
+        calls[0] += 1
+        return f(x, cs, sn, pos) if calls[0] % 2 == 1 else x   # forward rotates q, then k
+    monkeypatch.setattr(R, "rope_ht", g)
+
+
+def _plant_qk_swap(monkeypatch):
+    f = R.attention
+    monkeypatch.setattr(R, "attention", lambda q, k, v, *a, **kw: f(k, q, v, *a, **kw))
+
+
+def _plant_k_at_q_position(monkeypatch):
+    # scoring q_i against k_j rotated at position i instead of j: the same
+    # rotation on both sides cancels in the dot product, which is the
+    # forward with no rotation at all
+    monkeypatch.setattr(R, "rope_ht", lambda x, cs, sn, pos: x)
+
+
+def _plant_inverse_rotation(monkeypatch):
+    f = R.rope_ht
+    monkeypatch.setattr(R, "rope_ht", lambda x, cs, sn, pos: f(x, cs, -sn, pos))
+
+
+def _plant_no_qk_norm(monkeypatch):
+    f = R.rms
+    monkeypatch.setattr(R, "rms", lambda x, eps=1e-6: R.bf(x) if x.dim() == 4 else f(x, eps))
+
+
+QK_MUTATIONS = {
+    "scale 1/sqrt(Dh)": _plant_scale,
+    "RoPE on q only": _plant_rope_q_only,
+    "q<->k swapped": _plant_qk_swap,
+    "k rotated at q's position": _plant_k_at_q_position,
+    "inverse rotation": _plant_inverse_rotation,
+    "no QK-norm": _plant_no_qk_norm,
+}
+
+
+@pytest.mark.parametrize("mut", list(QK_MUTATIONS))
+def test_planted_qk_path_mistakes_fail(mut, monkeypatch):
+    p = _qk_params(7)
+    tok = _qk_tokens(12)
+    want = closed_form_qk_path(p, tok)
+    QK_MUTATIONS[mut](monkeypatch)
+    g = _gap(_oracle(p, tok, QK_CFG), want)
+    assert _differs(g), (mut, g)
