@@ -134,6 +134,26 @@ def test_prefill_logits_every_position_long_prompt(dh, window):
     assert err < LOGIT_TOL, err
 
 
+@pytest.mark.parametrize("dh,window", [(64, 70), (128, 100)])
+def test_prefill_bf16_p_within_both_oracle_readings(dh, window):
+    """The prefill attention rounds the softmax weights to bf16 before P.V.
+    Its logits at every position of a 300-token prompt stay within the 2e-2
+    bar of both oracle readings of model.py:251-254's attention: fp32 scores,
+    softmax and P.V (the default), and MLX's decomposed form (q pre-scaled in
+    bf16, bf16 scores and probabilities, bf16 P.V)."""
+    cfg = GPTConfig(vocab_size=700, num_layers=3, num_heads=2, model_dim=2 * dh, seq_len=320,
+                    window=window, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 29, dense=True))
+    tok = np.random.default_rng(dh * 3 + window).integers(0, cfg.vocab_size, (2, 300))
+    print(f"case dh={dh} window={window} B=2 T=300, both attention readings", flush=True)
+    eng = _engine(cfg, p, 2)
+    got = eng.forward_logits(tok).cpu()
+    for mlx in (False, True):
+        ref = R.logits(cfg, p, tok, mlx_fallback_attn=mlx)
+        err = (got - ref).abs().max().item()
+        assert err < LOGIT_TOL, (mlx, err)
+
+
 @pytest.mark.parametrize("d,B,T", [(512, 2, 300), (768, 3, 200)])
 def test_prefill_wide_tiles(d, B, T):
     """Prefill shapes on the large-tile GEMMs: M = B*T >= 512 rows, not a
