@@ -1,8 +1,10 @@
-// Persistent decode step for batch 1: embed, every layer, lm_head and the
-// greedy argmax of one token in ONE launch of G 512-thread work-groups, at
-// most one per CU, all resident at once (model.py:223-263 for T = 1,
-// sample.py:44-49 greedy).  The host picks G (3/4 of the CUs where the rows
-// fit: fewer work-groups exchange faster, measured).
+// Persistent decode step for 1 to 4 rows (BM): embed, every layer, lm_head
+// and the greedy argmax of one token per row in ONE launch of G 512-thread
+// work-groups, at most one per CU, all resident at once (model.py:223-263 for
+// T = 1, sample.py:44-49 greedy).  The host picks G (3/4 of the CUs where the
+// rows fit: fewer work-groups exchange faster, measured).  Every projection
+// row's weights are read once per step and applied to the BM rows held in
+// LDS; the attention runs one work-group per (row, head, split).
 //
 // Why: at batch 1 a decode step is ~57 dependent phases whose own work is a
 // few microseconds of weight streaming; as separate kernels every phase pays
@@ -695,11 +697,15 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
 int decode_persist_slots(int d) { return d <= 512 ? 1 : d <= 1024 ? 2 : d <= 1536 ? 3 : 0; }
 
+// Row counts above one run for d <= 1024 (two 16-byte weight slots per lane):
+// the row buffers and split partials of 2-4 rows at d 1536 leave the LDS
+// budget too few splits.
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long) {
   const int ud = decode_persist_slots(d);
-  if (B != 1 || ud == 0 || (Dh != 64 && Dh != 128) || d % 16 || V % 2 || V > 65536 || L > 50 ||
-      G < 1)
+  if (B < 1 || B > PD_MAX_B || ud == 0 || (B > 1 && ud > 2) || (Dh != 64 && Dh != 128) ||
+      d % 16 || V % 2 || V > 65536 || L > 50 || G < 1)
     return false;
+  if (decode_persist_lds(B, d, H, Dh, s_long) > PD_MAX_LDS) return false;
   const int d2 = d / 2, rd = 2 * PD_PW * PD_NW;
   auto rows = [&](int npairs) { return 2 * ((npairs + G - 1) / G); };
   if (rows(3 * d2) > rd || rows(2 * d) > rd || rows(d2) > PD_NW) return false;
@@ -725,7 +731,7 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hip
   static bool attr = false;
   if (!attr) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)(144 * 1024));
+                                             (int)PD_MAX_LDS);
     if (e != hipSuccess) return e;
     attr = true;
   }
@@ -739,20 +745,39 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hip
   return hipLaunchKernel(fn, dim3(G), dim3(PD_T), args, lds, st);
 }
 
+template <int BM>
+static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool coop,
+                              hipStream_t st) {
+  switch (Dh * 16 + decode_persist_slots(P.d)) {
+    case 64 * 16 + 1: return pd_launch<64, BM, 1>(P, G, lds, coop, st);
+    case 64 * 16 + 2: return pd_launch<64, BM, 2>(P, G, lds, coop, st);
+    case 128 * 16 + 1: return pd_launch<128, BM, 1>(P, G, lds, coop, st);
+    case 128 * 16 + 2: return pd_launch<128, BM, 2>(P, G, lds, coop, st);
+    default: break;
+  }
+  if constexpr (BM == 1) {   // three weight slots (d up to 1536): one row only
+    switch (Dh * 16 + decode_persist_slots(P.d)) {
+      case 64 * 16 + 3: return pd_launch<64, 1, 3>(P, G, lds, coop, st);
+      case 128 * 16 + 3: return pd_launch<128, 1, 3>(P, G, lds, coop, st);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st) {
   const size_t lds = decode_persist_lds(B, P.d, P.H, Dh, P.s_long);
-  if (lds > 144 * 1024 || B != 1) return hipErrorInvalidValue;
-  // o rows per work-group within what its registers hold
+  if (lds > PD_MAX_LDS || B < 1 || B > PD_MAX_B) return hipErrorInvalidValue;
+  // the attention work-groups leave at least one for the o rows, each within
+  // what its registers hold
   const int rd = 2 * PD_PW * PD_NW;
   const int no = P.on < G - B * P.H * P.s_long ? P.on : G - B * P.H * P.s_long;
   if (no < 1 || 2 * ((P.d / 2 + no - 1) / no) > rd) return hipErrorInvalidValue;
-  switch (Dh * 16 + decode_persist_slots(P.d)) {
-    case 64 * 16 + 1: return pd_launch<64, 1, 1>(P, G, lds, coop, st);
-    case 64 * 16 + 2: return pd_launch<64, 1, 2>(P, G, lds, coop, st);
-    case 64 * 16 + 3: return pd_launch<64, 1, 3>(P, G, lds, coop, st);
-    case 128 * 16 + 1: return pd_launch<128, 1, 1>(P, G, lds, coop, st);
-    case 128 * 16 + 2: return pd_launch<128, 1, 2>(P, G, lds, coop, st);
-    case 128 * 16 + 3: return pd_launch<128, 1, 3>(P, G, lds, coop, st);
+  switch (B) {
+    case 1: return pd_dispatch<1>(P, Dh, G, lds, coop, st);
+    case 2: return pd_dispatch<2>(P, Dh, G, lds, coop, st);
+    case 3: return pd_dispatch<3>(P, Dh, G, lds, coop, st);
+    case 4: return pd_dispatch<4>(P, Dh, G, lds, coop, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -78,16 +78,15 @@ struct SLayout {  // byte offsets into the workspace
       ce, ce_tz, ce_rows, ce_mean, total;
 };
 
-// Exchange area of the persistent decode step (batch 1): tagged words of
-// xq, xp, xm, xh, xx, xk, then the generation and error words; xm and xx
-// hold PD_MAX_REP copies pd_rep_stride words apart.  With `which` = 1..8
-// returns the byte offset of that part, 0 the total size.
-constexpr int PD_BATCH = 1;
+// Exchange area of the persistent decode step (up to PD_MAX_B rows): tagged
+// words of xq, xp, xm, xh, xx, xk, then the generation and error words; xm
+// and xx hold PD_MAX_REP copies pd_rep_stride words apart.  With `which` =
+// 1..8 returns the byte offset of that part, 0 the total size.
 constexpr int PD_MAX_SLONG = 8;
 constexpr int PD_MAX_G = 1024;
-size_t pd_rep_stride(const ann_config& c) { return ((size_t)PD_BATCH * c.d / 2 + 63) / 64 * 64; }
+size_t pd_rep_stride(const ann_config& c) { return ((size_t)PD_MAX_B * c.d / 2 + 63) / 64 * 64; }
 size_t pd_layout(const ann_config& c, int which) {
-  const size_t d = c.d, H = c.H, Dh = d / c.H, B = PD_BATCH, rs = pd_rep_stride(c);
+  const size_t d = c.d, H = c.H, Dh = d / c.H, B = PD_MAX_B, rs = pd_rep_stride(c);
   const size_t parts[8] = {B * 3 * d / 2, B * H * PD_MAX_SLONG * (Dh + 1), PD_MAX_REP * rs, B * 2 * d,
                            PD_MAX_REP * rs, (size_t)PD_MAX_G * B, 1, 1};
   size_t off = 0;
@@ -209,6 +208,12 @@ struct ann_ctx {
   // decode attention: splits per (row, head) fixed by ANN_DEC_SPLITS (0: sized
   // by the batch, about 384 work-groups)
   int dec_split_env = 0;
+  // rows the persistent step takes by default: its GEMV-style phases apply
+  // every weight to each row in turn, so a row costs ~60 us more (155M
+  // decode step at 1 / 2 / 3 / 4 rows: 185 / 256 / 308 / 370 us against
+  // 258 / 301 / 320 / 326 us on the per-kernel path, measured);
+  // ANN_PERSIST_MAX_B (1..PD_MAX_B) changes it
+  int pd_max_b = 3;
   int pd_rep = PD_MAX_REP;   // copies of the persistent step's x' / x exchange
   int pd_on = 0;             // work-groups for the o rows (0: d / 8, 8 rows each)
   // measurement: HIP event pairs around every launch of one kernel class
@@ -522,17 +527,27 @@ void drop_graph(ann_ctx* c) {
 
 // Splits per (b, h) of the persistent step's attention: about 128 keys per
 // work-group (one 16-key chunk per wave, issued before the wait for q/k/v).
+// Above one row the B * H * s attention work-groups leave the o projection
+// its d / 8 work-groups (ANN_PD_ON sets the count) and the split partials fit
+// the LDS beside the row buffers.
 int pd_splits(const ann_ctx* c, int B, bool lng) {
   const int keys = lng ? c->c.max_ctx : (c->c.window < c->c.max_ctx ? c->c.window : c->c.max_ctx);
   int s = (keys + 127) / 128;
   if (s > PD_MAX_SLONG) s = PD_MAX_SLONG;
   if (c->pd_g > 0 && s > c->pd_g / (B * c->c.H)) s = c->pd_g / (B * c->c.H);
+  if (B > 1 && c->pd_g > 0) {
+    const int on = c->pd_on > 0 ? c->pd_on : c->c.d / 8;
+    const int cap = (c->pd_g - on) / (B * c->c.H);
+    if (s > cap) s = cap;
+    while (s > 1 && decode_persist_lds(B, c->c.d, c->c.H, c->Dh, s) > PD_MAX_LDS) --s;
+  }
   return s < 1 ? 1 : s;
 }
 
 // Whether this decode step runs as the persistent kernel.
 bool persist_ok(ann_ctx* c, int B) {
-  if (!c->pd_env || B != PD_BATCH || (c->prof_kind >= 0 && c->prof_kind != ANN_PROF_STEP))
+  if (!c->pd_env || B < 1 || B > c->pd_max_b ||
+      (c->prof_kind >= 0 && c->prof_kind != ANN_PROF_STEP))
     return false;
   const ann_config& g = c->c;
   if (c->pd_g < 0) {
@@ -560,8 +575,7 @@ bool persist_ok(ann_ctx* c, int B) {
       for (int cand : cands) {
         if (cand < 1) continue;
         c->pd_g = cand;   // pd_splits reads it
-        if (decode_persist_fits(PD_BATCH, g.d, g.H, c->Dh, g.V, g.L, cand,
-                                pd_splits(c, PD_BATCH, true))) {
+        if (decode_persist_fits(1, g.d, g.H, c->Dh, g.V, g.L, cand, pd_splits(c, 1, true))) {
           pick = cand;
           break;
         }
@@ -696,6 +710,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   const char* ds = getenv("ANN_DEC_SPLITS");
   c->dec_split_env = ds ? atoi(ds) : 0;
   if (c->dec_split_env < 0 || c->dec_split_env > MAX_SPLIT) c->dec_split_env = 0;
+  const char* pm = getenv("ANN_PERSIST_MAX_B");
+  if (pm && atoi(pm) >= 1 && atoi(pm) <= PD_MAX_B) c->pd_max_b = atoi(pm);
   const char* pc = getenv("ANN_PERSIST_COOP");
   c->pd_coop = pc && pc[0] == '1';
   *out = c;

@@ -197,9 +197,9 @@ hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float 
 hipError_t set_pos(int32_t* pos, int B, int value, hipStream_t st);
 hipError_t advance_pos(int32_t* pos, int B, int n, hipStream_t st);
 
-// Persistent decode step (batch 1): one launch of G work-groups (one per
-// CU, all resident) runs embed, all layers, lm_head and (greedy) the argmax;
-// see decode_persist.hip.  Exchange words are 64-bit (tag << 32 | data).
+// Persistent decode step (1 .. PD_MAX_B rows): one launch of G work-groups
+// (one per CU, all resident) runs embed, all layers, lm_head and (greedy) the
+// argmax; see decode_persist.hip.  Exchange words are 64-bit (tag << 32 | data).
 typedef unsigned long long u64;
 struct PDParams {
   const bf16_t* emb;
@@ -232,6 +232,8 @@ struct PDParams {
   float scale, shift, eps;
 };
 constexpr int PD_MAX_REP = 8;
+constexpr int PD_MAX_B = 4;                       // rows of the persistent step
+constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffers + partials)
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
 hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st);

@@ -246,16 +246,19 @@ def test_forward_loss_equals_cross_entropy_of_own_logits():
 
 @pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 2), ("dh128", 4), ("dh128", 8),
                                     ("dh128", 12)])
-def test_decode_teacher_forced_past_window(name, B):
+def test_decode_teacher_forced_past_window(name, B, monkeypatch):
     """Decode logits at every position (well past the window) match the
-    oracle's KV-cache forward on the same tokens (two rows take the GEMV with
-    the fused greedy keys; 4, 8 and 12 rows the skinny MFMA GEMMs, the logits
-    GEMM and the sampler kernel, and the split-combine attention)."""
+    oracle's KV-cache forward on the same tokens, on the per-kernel path
+    (ANN_PERSIST=0: two rows take the GEMV with the fused greedy keys; 4, 8
+    and 12 rows the skinny MFMA GEMMs, the logits GEMM and the sampler kernel,
+    and the split-combine attention)."""
     cfg = small_cfgs()[name]
     p = perturb_lambdas(init_params(cfg, 5, dense=True))
     T0, steps = 7, cfg.seq_len - 7
     tok = np.random.default_rng(1).integers(0, cfg.vocab_size, (B, T0 + steps))
+    monkeypatch.setenv("ANN_PERSIST", "0")
     eng = _engine(cfg, p, B)
+    monkeypatch.delenv("ANN_PERSIST")
     prep = R.Prepared(cfg, p)
     cache = R.KVCache(cfg.num_layers)
     _, lg = eng.prefill(tok[:, :T0], want_logits=True)
@@ -269,16 +272,23 @@ def test_decode_teacher_forced_past_window(name, B):
     assert worst < LOGIT_TOL, worst
 
 
-@pytest.mark.parametrize("B", [4, 8])
-def test_decode_small_batch_sampled_matches_oracle(B):
-    """Sampled decode (T = 0.9, top-k 20) at 4 and 8 rows: the logits match
+@pytest.mark.parametrize("B,persist", [(3, True), (4, True), (4, False), (8, False)])
+def test_decode_small_batch_sampled_matches_oracle(B, persist, monkeypatch):
+    """Sampled decode (T = 0.9, top-k 20) at 3, 4 and 8 rows -- 3 and 4 rows on
+    the persistent step (its z rows, then the sampler kernel; 4 rows through
+    ANN_PERSIST_MAX_B), 4 and 8 rows on the per-kernel path: the logits match
     the oracle at every step and every row's draw equals the oracle sampler's
     draw (Philox counter (step, row)) from the engine's own logits."""
     cfg = small_cfgs()["dh128"]
     p = perturb_lambdas(init_params(cfg, 25, dense=True))
     T0, steps, temp, k, seed = 7, 30, 0.9, 20, 77
     tok = np.random.default_rng(3 + B).integers(0, cfg.vocab_size, (B, T0 + steps))
+    monkeypatch.setenv("ANN_PERSIST_MAX_B", "4")
+    if not persist:
+        monkeypatch.setenv("ANN_PERSIST", "0")
     eng = _engine(cfg, p, B)
+    monkeypatch.delenv("ANN_PERSIST", raising=False)
+    monkeypatch.delenv("ANN_PERSIST_MAX_B")
     prep = R.Prepared(cfg, p)
     cache = R.KVCache(cfg.num_layers)
     nxt, lg = eng.prefill(tok[:, :T0], temp, k, seed=seed, step=0, want_logits=True)
@@ -300,18 +310,25 @@ def test_decode_small_batch_sampled_matches_oracle(B):
             assert int(got[b]) == want, (step, b)
 
 
-def test_one_token_prompts_then_decode_match_oracle():
+@pytest.mark.parametrize("persist", [False, True])
+def test_one_token_prompts_then_decode_match_oracle(persist, monkeypatch):
     """Prompts of one token at 4 rows: the prefill's attention is then the
     decode kernel itself, with 8 key splits on the full-causal layers (ticket
     counters and tagged partials), so the decode steps after it continue from
-    the counters it left.  Logits match the oracle's KV-cache forward at every
-    step, and no bounded wait timed out."""
+    the counters it left (per-kernel path, ANN_PERSIST=0) or start the
+    persistent step from the exchange area it cleared.  Logits match the
+    oracle's KV-cache forward at every step, and no bounded wait timed out."""
     cfg = GPTConfig(vocab_size=1000, num_layers=3, num_heads=2, model_dim=256, seq_len=512,
                     window=8, long_layers=(0, 2))
     p = perturb_lambdas(init_params(cfg, 31, dense=True))
     B, steps = 4, 24
     tok = np.random.default_rng(31).integers(0, cfg.vocab_size, (B, 1 + steps))
+    monkeypatch.setenv("ANN_PERSIST_MAX_B", "4")
+    if not persist:
+        monkeypatch.setenv("ANN_PERSIST", "0")
     eng = _engine(cfg, p, B, ctx=512, tokens=4 * B)
+    monkeypatch.delenv("ANN_PERSIST", raising=False)
+    monkeypatch.delenv("ANN_PERSIST_MAX_B")
     prep = R.Prepared(cfg, p)
     cache = R.KVCache(cfg.num_layers)
     _, lg = eng.prefill(tok[:, :1], want_logits=True)
@@ -347,6 +364,69 @@ def test_persistent_decode_matches_oracle(name):
         worst = max(worst, (lg.cpu() - ref).abs().max().item())
     eng.check_device()
     assert worst < LOGIT_TOL, worst
+
+
+@pytest.mark.parametrize("name,B", [("dh64", 2), ("dh128", 3), ("dh128", 4)])
+def test_persistent_rows_decode_matches_oracle(name, B, monkeypatch):
+    """The persistent step at 2-4 rows (every projection row's weights applied
+    to the rows held in LDS, one attention work-group per (row, head, split);
+    4 rows through ANN_PERSIST_MAX_B): teacher-forced logits of every row at
+    every position, past the window, match the oracle, and no bounded wait
+    timed out."""
+    cfg = small_cfgs()[name]
+    p = perturb_lambdas(init_params(cfg, 17, dense=True))
+    T0, steps = 5, cfg.seq_len - 5
+    tok = np.random.default_rng(19 + B).integers(0, cfg.vocab_size, (B, T0 + steps))
+    monkeypatch.setenv("ANN_PERSIST_MAX_B", "4")
+    eng = _engine(cfg, p, B)
+    monkeypatch.delenv("ANN_PERSIST_MAX_B")
+    prep = R.Prepared(cfg, p)
+    cache = R.KVCache(cfg.num_layers)
+    _, lg = eng.prefill(tok[:, :T0], want_logits=True)
+    worst = (lg.cpu() - R.forward(prep, tok[:, :T0], cache)[:, -1]).abs().max().item()
+    for i in range(steps - 1):
+        t = tok[:, T0 + i]
+        _, lg = eng.decode(torch.from_numpy(t.astype(np.int32)).cuda(), want_logits=True)
+        ref = R.forward(prep, t[:, None], cache)[:, -1]
+        worst = max(worst, (lg.cpu() - ref).abs().max().item())
+    eng.check_device()
+    assert worst < LOGIT_TOL, worst
+
+
+def test_persistent_rows_match_kernel_path(monkeypatch):
+    """3 rows: the persistent step and the per-kernel step (ANN_PERSIST=0)
+    give identical greedy tokens in every row over 60 steps and logits within
+    the oracle tolerance (they sum in different orders); seeded top-k draws
+    of the persistent step equal the oracle sampler's draws from the step's
+    own logits."""
+    cfg = small_cfgs()["dh128"]
+    p = perturb_lambdas(init_params(cfg, 27, dense=True))
+    prompt = np.random.default_rng(14).integers(0, cfg.vocab_size, (3, 6))
+
+    def run(persist, temp, k):
+        if not persist:
+            monkeypatch.setenv("ANN_PERSIST", "0")
+        eng = _engine(cfg, p, 3)
+        monkeypatch.delenv("ANN_PERSIST", raising=False)
+        nxt, _ = eng.prefill(prompt, temp, k, seed=9, step=0)
+        toks, lgs = [nxt.cpu().numpy().copy()], []
+        for i in range(60):
+            nxt, lg = eng.decode(nxt, temp, k, seed=9, step=i + 1, want_logits=True)
+            toks.append(nxt.cpu().numpy().copy())
+            lgs.append(lg.cpu())
+        eng.check_device()
+        return np.stack(toks), torch.stack(lgs)
+
+    ta, la = run(True, 0.0, 0)
+    tb, lb = run(False, 0.0, 0)
+    assert np.array_equal(ta, tb)
+    assert (la - lb).abs().max().item() < LOGIT_TOL
+    temp, k = 0.9, 20
+    sa, ls = run(True, temp, k)
+    for i in range(60):
+        for b in range(3):
+            z = ls[i, b].numpy()[:min(50257, cfg.vocab_size)]
+            assert sa[i + 1, b] == _sample_small(z, temp, k, S.uniform(9, i + 1, b)), (i, b)
 
 
 def test_persistent_cooperative_launch(monkeypatch):
@@ -620,6 +700,35 @@ def test_greedy_155m_identical_64_steps():
     worst = max((g - r).abs().max().item() for g, r in zip(glog[:n_same], rlog[:n_same]))
     assert worst < LOGIT_TOL, worst
     assert got == ref, f"first divergence at step {n_same}"
+
+
+@pytest.mark.parametrize("B", [3, 4])
+def test_greedy_155m_rows_identical_to_oracle(B, monkeypatch):
+    """The 155M model, three and four independent sequences on the
+    persistent step (four through ANN_PERSIST_MAX_B): 32-token prompts, 32
+    greedy steps, every row's tokens identical to the oracle's greedy decode
+    of that row and its logits within 2e-2."""
+    cfg = cfg_155m()
+    p = init_params(cfg, 4, dense=True)
+    prompts = np.random.default_rng(44).integers(0, 50257, (B, 32))
+    monkeypatch.setenv("ANN_PERSIST_MAX_B", "4")
+    eng = _engine(cfg, p, B, ctx=1024, tokens=B * 32)
+    monkeypatch.delenv("ANN_PERSIST_MAX_B")
+    print(f"case 155M, {B} rows, 32 greedy steps", flush=True)
+    nxt, lg = eng.prefill(prompts, want_logits=True)
+    got, glog = [nxt.cpu().numpy().copy()], [lg.cpu()]
+    for _ in range(31):
+        nxt, lg = eng.decode(nxt, want_logits=True, out=nxt)
+        got.append(nxt.cpu().numpy().copy())
+        glog.append(lg.cpu())
+    eng.check_device()
+    got = np.stack(got)
+    for b in range(B):
+        ref, rlog = _greedy_oracle(cfg, p, prompts[b], 32)
+        n_same = next((i for i, (a, r) in enumerate(zip(got[:, b], ref)) if a != r), 32)
+        worst = max((glog[i][b] - rlog[i]).abs().max().item() for i in range(n_same))
+        assert worst < LOGIT_TOL, (b, worst)
+        assert list(got[:, b]) == ref, f"row {b}: first divergence at step {n_same}"
 
 
 def test_persistent_155m_late_positions_match_oracle():
