@@ -515,13 +515,15 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < PD_NW; ++w) o += s_o[w][tid];
-        ll_store(dst + tid, __float_as_uint(o), t1 + 1u);
+        for (int c = 0; c < PD_REP_P; ++c)
+          ll_store(dst + (size_t)c * P.p_stride + tid, __float_as_uint(o), t1 + 1u);
       }
       if (tid == 0) {
         float lt = 0.f;
 #pragma unroll
         for (int w = 0; w < PD_NW; ++w) lt += s_l[w];
-        ll_store(dst + DH, __float_as_uint(lt), t1 + 1u);
+        for (int c = 0; c < PD_REP_P; ++c)
+          ll_store(dst + (size_t)c * P.p_stride + DH, __float_as_uint(lt), t1 + 1u);
       }
     }
 
@@ -534,7 +536,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     // the exchange.
     if (!attn) {
       const int nw = BM * H * S * (DH + 1);
-      ll_poll(P.xp, nw, (uint32_t*)spart, t1 + 1u, P.err);
+      ll_poll(P.xp + (size_t)(g % PD_REP_P) * P.p_stride, nw, (uint32_t*)spart, t1 + 1u, P.err);
       __syncthreads();
       for (int i = tid; i < BM * d; i += PD_T) {
         const int b = i / d, c = i - b * d, h = c / DH, e = c - h * DH;
@@ -558,12 +560,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     __syncthreads();
     pd_rms<BM>(sxm, gin, d, P.eps, red);
     pd_wdot2<PE_RELU2, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr,
-                               nullptr, d, 1, 0);
+                               nullptr, d, PD_REP_H, P.h_stride);
 
     // ---- 5: x = mix_mlp(x', h Wproj^T)
     pd_rows(d2, n0, nr, 0, G);
     pd_wload<4 * UD, 1>(Wl + P.o_proj, 4 * d, n0, nr, wr);
-    ll_poll(P.xh, BM * 2 * d, (uint32_t*)ghb, t1 + 3u, P.err);
+    ll_poll(P.xh + (size_t)(g % PD_REP_H) * P.h_stride, BM * 2 * d, (uint32_t*)ghb, t1 + 3u, P.err);
     __syncthreads();
     pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)ghb, 4 * d, nr, stage);
     pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d, P.rep, P.rep_stride);

@@ -219,19 +219,27 @@ struct PDParams {
   bf16_t* z;              // !greedy: bf16 logits (B, V)
   float* logits;          // optional fp32 softcapped logits (B, V)
   u64* xq;                // qkv       B x 3d/2 words
-  u64* xp;                // partials  B*H*s_long x (Dh+1)
+  u64* xp;                // partials  PD_REP_P copies of B*H*s_long x (Dh+1), p_stride apart
   u64* xm;                // x'        rep copies of B x d/2, rep_stride words apart
-  u64* xh;                // hidden    B x 2d
+  u64* xh;                // hidden    PD_REP_H copies of B x 2d, h_stride words apart
   u64* xx;                // x         rep copies of B x d/2, rep_stride words apart
   u64* xk;                // keys      G x B
   unsigned* gen;          // step generation (tags)
   unsigned* err;          // set when a bounded wait timed out
   int d, H, L, V, Vs, max_ctx, window, s_win, s_long, greedy;
   int rep, rep_stride;    // copies of xm / xx (1..PD_MAX_REP); work-group g reads copy g % rep
+  int h_stride;           // xh: PD_REP_H copies, work-group g reads copy g % PD_REP_H
+  int p_stride;           // xp: PD_REP_P copies, work-group g reads copy g % PD_REP_P
   int on;                 // work-groups holding the o rows (at most, after the attention ones)
   float scale, shift, eps;
 };
 constexpr int PD_MAX_REP = 8;
+// Copies of the h and attention-partial exchanges (their areas hold up to
+// PD_MAX_REP).  Fewer pollers per copy: the 155M batch-1 generation 181.4 ->
+// 178.8 and 178.4 -> 176.8 ms (two boxes, alternating A/B) with 4 of each
+// against one; 8 h / 4 partial copies 179.9.  Compile-time counts: the same
+// copies chosen at run time measured 6% slower (loops and modulo in the step).
+constexpr int PD_REP_H = 4, PD_REP_P = 4;
 constexpr int PD_MAX_B = 4;                       // rows of the persistent step
 constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffers + partials)
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
