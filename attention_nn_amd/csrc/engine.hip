@@ -191,7 +191,12 @@ struct ann_ctx {
     int32_t* out;
     float* logits;
     bool greedy;
+    bool cand;
   } gkey{};
+  bool cand_env = true;  // ANN_TOPK_CAND=0: the lm_head always stores z for the sampler
+  // ANN_TOPK_VERIFY=1: the candidate sampler recomputes every lm_head tile and
+  // flags (ann_check_device) any difference from the GEMM's candidates
+  bool cand_verify = false;
   // host mirror of the device sampling parameters
   bool sp_valid = false;
   float sp_temp = 0.f;
@@ -271,7 +276,7 @@ bool proj_is_gemm(int M, int N, int K, int pre) {
 int proj(ann_ctx* c, int kind, int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx,
          int M, int N, int K, EpiArgs ea, hipStream_t st) {
   // the QKV and CE epilogues exist on the MFMA GEMM only
-  const bool gemm_only = epi == EPI_CE;
+  const bool gemm_only = epi == EPI_CE || epi == EPI_TOPK;
   const bool use_gemv = !gemm_only && gemv_routes(M, K);
   const bool use_sk = !gemm_only && !use_gemv && !proj_is_gemm(M, N, K, pre);
   if (epi == EPI_QKV && (use_gemv || use_sk)) return fail(ANN_E_ARG, "fused QKV needs the MFMA GEMM");
@@ -475,6 +480,20 @@ int check_sampling(const ann_ctx* c, const ann_sampling* s) {
 // z of the last row of each sequence -> sampled token; positions advance by
 // pos_adv (the tokens this call added).  Sampling parameters come from the
 // device copy written by sync_sampling.
+// The device error word: bounded waits that gave up (bit 0), the candidate
+// sampler's check (bit 1).
+unsigned* dec_err_word(ann_ctx* c) { return (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8)); }
+
+// The lm_head stores top-k candidates (EPI_TOPK) and sample_cand draws from
+// them -- no z -- where the MFMA GEMM takes the lm_head (3 .. 511 rows; up
+// to 2 rows the GEMV keeps its own argmax keys) for greedy rows and for
+// 1 <= top_k <= 256; top_k 0 (every entry kept) or larger samples from z.
+bool cand_route(const ann_ctx* c, int B, bool greedy) {
+  const ann_config& g = c->c;
+  if (!c->cand_env || B >= 512 || !proj_is_gemm(B, g.V, g.d, PRE_RMS) || g.V > 65536) return false;
+  return greedy || (c->sp_topk >= 1 && c->sp_topk <= 256 && c->sp_topk < g.V_sample);
+}
+
 int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, float* logits,
                     int pos_adv, hipStream_t st) {
   const ann_config& g = c->c;
@@ -484,6 +503,25 @@ int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, flo
   EpiArgs ez{};
   ez.logits = logits;
   ez.ldz = g.V;
+  if (cand_route(c, B, greedy)) {
+    // candidates in the z area: (B, nt, TK_M) words, then (B, nt)
+    const int nt = ce_tiles(g);
+    uint32_t* cand = (uint32_t*)zb;
+    uint32_t* cand_r = cand + (size_t)B * nt * TK_M;
+    ez.cand = cand;
+    ez.cand_r = cand_r;
+    ez.nt = nt;
+    ez.Vs = g.V_sample;
+    int rc = proj(c, ANN_PROF_LM_HEAD, EPI_TOPK, PRE_RMS, c->wptr(c->wl.head),
+                  x + (size_t)(T - 1) * g.d, T * g.d, B, g.V, g.d, ez, st);
+    if (rc) return rc;
+    // the GEMM's A operand: the rows normalised into hn by proj()
+    HIPCHK(sample_cand(cand, cand_r, nt, B, g.V_sample, c->sp<bf16_t>(c->sl.hn), g.d,
+                       c->wptr(c->wl.head), g.V, g.d, c->sp<SampParams>(c->sl.sp),
+                       c->sp<unsigned long long>(c->sl.steps), out_tok, pos, pos_adv,
+                       c->cand_verify ? dec_err_word(c) : nullptr, st));
+    return ANN_OK;
+  }
   const bool fused_greedy = greedy && gemv_routes(B, g.d);
   unsigned long long* keys = c->sp<unsigned long long>(c->sl.amax);
   if (fused_greedy) {
@@ -668,10 +706,10 @@ int enqueue_decode(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_
 // Capture one decode step into a graph (once per key) and launch it.
 int decode_graph(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32_t* out_tok,
                  float* logits, hipStream_t st) {
-  const ann_ctx::GKey key{B, tokens, out_tok, logits, greedy};
+  const ann_ctx::GKey key{B, tokens, out_tok, logits, greedy, cand_route(c, B, greedy)};
   const bool same = c->gexec && key.B == c->gkey.B && key.tok == c->gkey.tok &&
                     key.out == c->gkey.out && key.logits == c->gkey.logits &&
-                    key.greedy == c->gkey.greedy;
+                    key.greedy == c->gkey.greedy && key.cand == c->gkey.cand;
   if (!same) {
     drop_graph(c);
     if (!c->cap_st) HIPCHK(hipStreamCreateWithFlags(&c->cap_st, hipStreamNonBlocking));
@@ -721,6 +759,10 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   if (c->dec_split_env < 0 || c->dec_split_env > MAX_SPLIT) c->dec_split_env = 0;
   const char* pm = getenv("ANN_PERSIST_MAX_B");
   if (pm && atoi(pm) >= 1 && atoi(pm) <= PD_MAX_B) c->pd_max_b = atoi(pm);
+  const char* tc = getenv("ANN_TOPK_CAND");
+  c->cand_env = !(tc && tc[0] == '0');
+  const char* tv = getenv("ANN_TOPK_VERIFY");
+  c->cand_verify = tv && tv[0] == '1';
   const char* pc = getenv("ANN_PERSIST_COOP");
   c->pd_coop = pc && pc[0] == '1';
   *out = c;
@@ -770,11 +812,13 @@ int ann_check_device(ann_ctx* c, void* stream) {
   if (rc) return rc;
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
   if (c->dec_clear) return ANN_OK;   // no decode-state user has run since binding
-  unsigned* err = (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8));
+  unsigned* err = dec_err_word(c);
   unsigned h = 0;
   HIPCHK(hipMemcpy(&h, err, sizeof h, hipMemcpyDeviceToHost));
   if (h) {
     HIPCHK(hipMemset(err, 0, sizeof h));
+    if (h & 2u)
+      return fail(ANN_E_HIP, "sampler check: recomputed lm_head keys differ from the candidates");
     return fail(ANN_E_HIP, "decode step: a bounded cross-work-group wait timed out");
   }
   return ANN_OK;

@@ -21,12 +21,22 @@ namespace ann {
 //                   128-column tile t: ce_part[t * ldz + m] = sum of exp(softcap(bf16(y)))
 //                   over the tile's columns; ce_tz[m] = softcap(bf16(y[tgt[m]])) from
 //                   the tile holding the target (metal_kernels.py:153-193)
+//   EPI_TOPK        (MFMA GEMM only, decode lm_head of 3..256 rows) per row m and
+//                   128-column tile t, over the columns n < Vs: the tile's 8
+//                   largest words (zkey(bf16(y)) << 16 | 0xffff - n, so equal
+//                   keys rank the lower column first) to cand[(m nt + t) 8 ..],
+//                   largest first (0 past the valid columns), and its 9th
+//                   largest word to cand_r[m nt + t]; softcap(z) -> logits fp32
+//                   (if set).  No z is stored (sample.py:44-49 via sample_cand)
 //   EPI_PE_B        (Polar Express) out = bf16(bf16(s0*x) + bf16(s1*bf16(y)))  (muon.py:37)
 //   EPI_PE_X        (Polar Express) out = bf16(bf16(s0*x) + bf16(y))           (muon.py:38,42)
 //                   x is the epilogue's second operand (M, ldr); when outT is set
 //                   the same values also go to outT (N, ldoT), transposed
 enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID_ATTN = 2, EPI_RESID_MLP = 3, EPI_LOGITS = 4,
-       EPI_QKV = 5, EPI_CE = 6, EPI_PE_B = 7, EPI_PE_X = 8 };
+       EPI_QKV = 5, EPI_CE = 6, EPI_PE_B = 7, EPI_PE_X = 8, EPI_TOPK = 9 };
+
+// Candidates a 128-column lm_head tile emits per row (EPI_TOPK).
+constexpr int TK_M = 8;
 
 struct EpiArgs {
   bf16_t* out;       // STORE / RELU2 output (M, ldo)
@@ -43,6 +53,10 @@ struct EpiArgs {
   // amax[m * blocks + block]; argmax_finalize turns them into tokens.
   unsigned long long* amax;
   int Vs;
+  // TOPK: candidate words (M, nt, TK_M) and 9th-largest words (M, nt)
+  uint32_t* cand;
+  uint32_t* cand_r;
+  int nt;
   // QKV: row m = b * T + t; model dim d = H * Dh; caches [B][H][max_ctx][Dh]
   bf16_t* kc;
   bf16_t* vc;
@@ -191,6 +205,18 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
 hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
                   unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
                   hipStream_t st);
+// The same draw from the lm_head's EPI_TOPK candidates (cand, cand_r: B rows of
+// nt tiles) instead of z.  Where the candidates cannot prove the kept set
+// complete (ties or clusters beyond TK_M keys in a tile, top_k 0 or above the
+// candidates) the work-group recomputes the tiles concerned from A (the
+// lm_head's normalised input rows, lda) and W (N x K) with the GEMM's MFMA
+// sequence, bit-identical z, and samples over the whole row.  verify (null
+// normally): recompute every tile and set bit 1 of *verify where a tile's
+// top TK_M + 1 words differ from the candidates.
+hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int B, int Vs,
+                       const bf16_t* A, int lda, const bf16_t* W, int N, int K,
+                       const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
+                       int32_t* pos, int pos_adv, unsigned* verify, hipStream_t st);
 hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
                         int top_k, unsigned long long seed, unsigned long long step,
                         hipStream_t st);

@@ -391,6 +391,107 @@ hipError_t gemv(int epi, int pre, const bf16_t* W, const bf16_t* X, int ldx, int
   return hipErrorInvalidValue;
 }
 
+// ---- lm_head top-k candidates (EPI_TOPK) ------------------------------------
+
+// max of v over the 16 lanes of each DPP row (lanes 16r .. 16r + 15): quad
+// swaps 1 and 2, then the half-row and row mirrors
+__device__ __forceinline__ uint32_t row16_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// descending compare-exchange
+__device__ __forceinline__ void cas_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = max(a, b), lo = min(a, b);
+  a = hi;
+  b = lo;
+}
+
+// Candidates of a staged bf16 tile (BM x 128, row pitch CP) of lm_head
+// outputs at (m0, n0), column tile tn.  A 16-lane row of the wave takes one
+// output row, 8 columns per lane, RP rows at a time (independent chains).
+// Each lane sorts its words (zkey << 16 | 0xffff - n; distinct, as the
+// columns are) in descending order; nine rounds of a row maximum over the
+// lanes' first words then pop the largest word from its lane: rounds 0-7 are
+// the candidates, largest first, round 8 the 9th largest word (0 when fewer
+// valid columns remain).  The fp32 softcapped logits are stored from the
+// same tile when requested.
+template <int BM, int CP>
+__device__ __forceinline__ void topk_tile_epilogue(const EpiArgs& ea, const bf16_t* tile, int m0,
+                                                   int n0, int M, int N, int tn, int tid) {
+  constexpr int RP = 4;
+  static_assert(BM % (16 * RP) == 0, "whole row groups");
+  const int grp = tid >> 4, li = tid & 15;
+  const int nb = n0 + li * 8;
+#pragma unroll 1
+  for (int p = 0; p < BM / 16; p += RP) {
+    uint32_t w[RP][8];
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      const int ml = (p + q) * 16 + grp, m = m0 + ml;
+      const uint4 v = *(const uint4*)(tile + ml * CP + li * 8);
+      const uint32_t hw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bf16_t h = (bf16_t)(e & 1 ? hw[e >> 1] >> 16 : hw[e >> 1] & 0xffffu);
+        w[q][e] = nb + e < ea.Vs ? (zkey(h) << 16) | (0xffffu - (uint32_t)(nb + e)) : 0u;
+      }
+      if (ea.logits && m < M) {
+        float* lr = ea.logits + (size_t)m * ea.ldz + nb;
+        if (nb + 7 < N && (ea.ldz & 3) == 0) {
+          float f[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            f[e] = softcap(__uint_as_float(e & 1 ? hw[e >> 1] & 0xffff0000u : hw[e >> 1] << 16));
+          *(float4*)lr = make_float4(f[0], f[1], f[2], f[3]);
+          *(float4*)(lr + 4) = make_float4(f[4], f[5], f[6], f[7]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (nb + e < N)
+              lr[e] = softcap(__uint_as_float(e & 1 ? hw[e >> 1] & 0xffff0000u : hw[e >> 1] << 16));
+        }
+      }
+      // Batcher's odd-even merge sort of 8, descending
+      uint32_t(&x)[8] = w[q];
+      cas_desc(x[0], x[1]); cas_desc(x[2], x[3]); cas_desc(x[4], x[5]); cas_desc(x[6], x[7]);
+      cas_desc(x[0], x[2]); cas_desc(x[1], x[3]); cas_desc(x[4], x[6]); cas_desc(x[5], x[7]);
+      cas_desc(x[1], x[2]); cas_desc(x[5], x[6]);
+      cas_desc(x[0], x[4]); cas_desc(x[1], x[5]); cas_desc(x[2], x[6]); cas_desc(x[3], x[7]);
+      cas_desc(x[2], x[4]); cas_desc(x[3], x[5]);
+      cas_desc(x[1], x[2]); cas_desc(x[3], x[4]); cas_desc(x[5], x[6]);
+    }
+    uint32_t mine[RP];   // lane li < 8: candidate li; lane 8: the 9th word
+#pragma unroll
+    for (int q = 0; q < RP; ++q) mine[q] = 0u;
+#pragma unroll
+    for (int r = 0; r <= TK_M; ++r) {
+#pragma unroll
+      for (int q = 0; q < RP; ++q) {
+        const uint32_t g = row16_max(w[q][0]);
+        if (li == r) mine[q] = g;
+        if (r < TK_M && w[q][0] == g) {
+#pragma unroll
+          for (int e = 0; e < 7; ++e) w[q][e] = w[q][e + 1];
+          w[q][7] = 0u;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      const int m = m0 + (p + q) * 16 + grp;
+      if (m < M) {
+        const size_t rec = (size_t)m * ea.nt + tn;
+        if (li < TK_M) ea.cand[rec * TK_M + li] = mine[q];
+        else if (li == TK_M) ea.cand_r[rec] = mine[q];
+      }
+    }
+  }
+}
+
 // ---- MFMA GEMM, large M (prefill) -------------------------------------------
 //
 // 128 x 128 x 64 block tiles, 4 waves of 64 x 64 (4 x 4 blocks of
@@ -428,12 +529,14 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   constexpr int CH = AC > BC ? AC : BC;
   // the QKV and CE epilogues work on 128-column tiles (whole heads; the
   // per-tile partial sums of the loss)
-  static_assert((EPI != EPI_QKV && EPI != EPI_CE) || BN == GM_BN, "128-column tiles");
+  static_assert((EPI != EPI_QKV && EPI != EPI_CE && EPI != EPI_TOPK) || BN == GM_BN,
+                "128-column tiles");
   // staged epilogues (QKV; PE_B / PE_X on full tiles) reuse the LDS for a bf16
   // BM x BN tile of row pitch BN + 8
   // the batched plain store stages its 128 x 128 tiles for the symmetric form
   constexpr bool STAGE_STORE = EPI == EPI_STORE && BM == GM_BM && BN == GM_BN && DEPTH == 1;
-  constexpr bool STAGED = EPI == EPI_QKV || EPI == EPI_PE_B || EPI == EPI_PE_X || STAGE_STORE;
+  constexpr bool STAGED =
+      EPI == EPI_QKV || EPI == EPI_PE_B || EPI == EPI_PE_X || EPI == EPI_TOPK || STAGE_STORE;
   constexpr int SMEM = (BM + BN) * GM_BK > (STAGED ? BM * (BN + 8) : 0)
                            ? (BM + BN) * GM_BK
                            : BM * (BN + 8);
@@ -698,6 +801,19 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
       }
     __syncthreads();
     qkv_tile_epilogue<BM, GM_BN + 8>(ea, smem, m0, n0, M, tid, pr);
+  } else if constexpr (EPI == EPI_TOPK) {
+    __syncthreads();   // every wave is done with the last K tile in LDS
+    constexpr int CP = BN + 8;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const floatx4_t y = acc[j][i];
+        *(uint2*)(smem + (wm * WM + i * 16 + r16) * CP + wn * WN + j * 16 + (lane >> 4) * 4) =
+            make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+      }
+    __syncthreads();
+    topk_tile_epilogue<BM, CP>(ea, smem, m0, n0, M, N, tn, tid);
   } else {
     if constexpr (EPI == EPI_PE_B || EPI == EPI_PE_X) {
       // full tiles with 16-byte rows: x prefetched before the staging
@@ -1389,6 +1505,13 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
     case EPI_CE:
       if (!ea.ce_part || !ea.ce_tz || !ea.tgt || ea.ldz < M) return hipErrorInvalidValue;
       ANN_GM_ONE(EPI_CE, shape)
+      break;
+    case EPI_TOPK:
+      // decode rows only (the 64- and 128-row tiles); every column tile one record
+      if (shape > 1 || !ea.cand || !ea.cand_r || ea.nt != (int)grid.x || ea.Vs < 1 ||
+          ea.Vs > N || N > 65536 || (ea.logits && ea.ldz < N))
+        return hipErrorInvalidValue;
+      ANN_GM_ONE(EPI_TOPK, shape)
       break;
     default:
       return hipErrorInvalidValue;

@@ -125,11 +125,15 @@ __device__ __forceinline__ uint32_t block_sum_waves(uint32_t wc, uint32_t* buf) 
   return t;
 }
 
-__global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
-                                                        int Vs, const SampParams* __restrict__ sp,
-                                                        unsigned long long* __restrict__ steps,
-                                                        int32_t* __restrict__ out_tok,
-                                                        int32_t* __restrict__ pos, int pos_adv) {
+// The draw for one row from the ordered 16-bit keys of this thread's entries
+// [base, base + nvalid), base = 56 tid (key 0 past the valid entries): the
+// whole-row sampler of k_sample, shared with k_sample_cand's fallback.
+__device__ __forceinline__ void sample_keys_row(uint32_t (&kk)[SMP_PER / 2], int Vs, int row,
+                                                float temperature, int top_k, uint64_t seed,
+                                                uint64_t step, int32_t pos0,
+                                                unsigned long long* __restrict__ steps,
+                                                int32_t* __restrict__ out_tok,
+                                                int32_t* __restrict__ pos, int pos_adv) {
   __shared__ uint32_t s_cnt[2][SMP_THREADS / 64];
   __shared__ uint64_t s_red[SMP_THREADS / 64];
   __shared__ uint32_t s_mm[2][SMP_THREADS / 64];
@@ -138,35 +142,9 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   __shared__ __attribute__((aligned(16))) unsigned short s_lmax[SMP_THREADS];
   __shared__ __attribute__((aligned(16))) unsigned short s_list[SMP_CAP];
   __shared__ uint32_t s_sel[2];   // [0] bound / threshold broadcast, [1] list length
-  const float temperature = sp->temperature;
-  const int top_k = sp->top_k;
-  const uint64_t seed = sp->seed;
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // this row's position and step, read now rather than behind the last barrier
-  const int32_t pos0 = pos ? pos[row] : 0;
-  const uint64_t step = steps[row];
-  const bf16_t* z = zall + (size_t)row * ldz;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int base = tid * SMP_PER;
   const int nvalid = max(0, min(SMP_PER, Vs - base));
-
-  // ---- keys of this thread's entries; entries >= Vs get key 0.  A chunk
-  // that starts below Vs lies inside the row's padded width (ldz >= Vs
-  // rounded up to 8, checked on the host).
-  uint32_t kk[SMP_PER / 2];
-#pragma unroll
-  for (int c = 0; c < SMP_CH; ++c) {
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (c * 8 < nvalid) v = *(const uint4*)(z + base + c * 8);
-    kk[4 * c + 0] = okey2(v.x);
-    kk[4 * c + 1] = okey2(v.y);
-    kk[4 * c + 2] = okey2(v.z);
-    kk[4 * c + 3] = okey2(v.w);
-  }
-  if (nvalid < SMP_PER) {
-#pragma unroll
-    for (int j = 0; j < SMP_PER / 2; ++j)
-      kk[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
-  }
   uint32_t lmax = 0;
   int lidx = 0;
 #pragma unroll
@@ -376,6 +354,375 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
   }
 }
 
+__global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict__ zall, int ldz,
+                                                        int Vs, const SampParams* __restrict__ sp,
+                                                        unsigned long long* __restrict__ steps,
+                                                        int32_t* __restrict__ out_tok,
+                                                        int32_t* __restrict__ pos, int pos_adv) {
+  const float temperature = sp->temperature;
+  const int top_k = sp->top_k;
+  const uint64_t seed = sp->seed;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  // this row's position and step, read now rather than behind the last barrier
+  const int32_t pos0 = pos ? pos[row] : 0;
+  const uint64_t step = steps[row];
+  const bf16_t* z = zall + (size_t)row * ldz;
+  const int base = tid * SMP_PER;
+  const int nvalid = max(0, min(SMP_PER, Vs - base));
+
+  // ---- keys of this thread's entries; entries >= Vs get key 0.  A chunk
+  // that starts below Vs lies inside the row's padded width (ldz >= Vs
+  // rounded up to 8, checked on the host).
+  uint32_t kk[SMP_PER / 2];
+#pragma unroll
+  for (int c = 0; c < SMP_CH; ++c) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (c * 8 < nvalid) v = *(const uint4*)(z + base + c * 8);
+    kk[4 * c + 0] = okey2(v.x);
+    kk[4 * c + 1] = okey2(v.y);
+    kk[4 * c + 2] = okey2(v.z);
+    kk[4 * c + 3] = okey2(v.w);
+  }
+  if (nvalid < SMP_PER) {
+#pragma unroll
+    for (int j = 0; j < SMP_PER / 2; ++j)
+      kk[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
+  }
+  sample_keys_row(kk, Vs, row, temperature, top_k, seed, step, pos0, steps, out_tok, pos,
+                  pos_adv);
+}
+
+// ---- draws from the lm_head's top-k candidates -------------------------------
+//
+// Each 128-column tile t of the lm_head left, per row, its TK_M largest words
+// (key << 16 | 0xffff - n, largest first) and its next largest word r_t
+// (EPI_TOPK).  Thread t holds tile t's candidates.  The k-th largest
+// candidate key T is found like k_sample's threshold (a lower bound from the
+// tile maxima, the keys above it listed and bisected).  If every tile's next
+// key r_t lies below the kept threshold tk (<= T), every key >= tk is a
+// candidate: the k-th largest key of the row is T (any larger k-th key would
+// have k candidates above T) and the kept set is the candidates >= tk.
+// Otherwise the tiles with r_t >= tk (all tiles when T could not be formed)
+// are recomputed into an LDS row of keys -- the others contribute their
+// candidates, the rest of their keys lying below tk and below any threshold
+// the full row can give -- and k_sample's whole-row draw runs on that row.
+// The recomputation repeats the lm_head GEMM's accumulation for the row: one
+// v_mfma_f32_16x16x32_bf16 per 32-wide k step in k order, W as the first
+// operand, the row as column 0 of the second, so z is bit-identical.
+// (Measured: the draw from the candidates in one wave, without block
+// barriers, took 14-15 us at 64 rows against 10 us for this form -- one wave
+// issues the counting at a quarter of the CU's VALU rate.)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+// ascending compare-exchange
+__device__ __forceinline__ void cas(uint32_t& a, uint32_t& b) {
+  const uint32_t lo = min(a, b), hi = max(a, b);
+  a = lo;
+  b = hi;
+}
+
+__global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
+    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_r, int nt, int Vs,
+    const bf16_t* __restrict__ A, int lda, const bf16_t* __restrict__ W, int N, int K,
+    const SampParams* __restrict__ sp, unsigned long long* __restrict__ steps,
+    int32_t* __restrict__ out_tok, int32_t* __restrict__ pos, int pos_adv,
+    unsigned* __restrict__ verify) {
+  extern __shared__ __attribute__((aligned(16))) unsigned short s_row[];   // nt * 128 keys
+  __shared__ uint32_t s_mx[3][SMP_THREADS / 64];
+  __shared__ uint32_t s_cnt[2][SMP_THREADS / 64];
+  __shared__ float s_wsum[SMP_THREADS / 64];
+  __shared__ uint32_t s_misc[2];
+  __shared__ __attribute__((aligned(16))) unsigned short s_lmax[SMP_THREADS];
+  __shared__ __attribute__((aligned(16))) unsigned short s_list[SMP_CAP];
+  __shared__ uint32_t s_sel[2];
+  __shared__ uint32_t s_nf;
+  __shared__ unsigned short s_flag[SMP_THREADS];
+  const float temperature = sp->temperature;
+  const int top_k = sp->top_k;
+  const uint64_t seed = sp->seed;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int32_t pos0 = pos ? pos[row] : 0;
+  const uint64_t step = steps[row];
+  const int holders = (Vs + 127) / 128;   // tiles with valid columns
+  uint32_t cw[TK_M], rw = 0u;
+  if (tid < holders) {
+    const uint4* src = (const uint4*)(cand + ((size_t)row * nt + tid) * TK_M);
+    const uint4 a = src[0], b = src[1];
+    cw[0] = a.x; cw[1] = a.y; cw[2] = a.z; cw[3] = a.w;
+    cw[4] = b.x; cw[5] = b.y; cw[6] = b.z; cw[7] = b.w;
+    rw = cand_r[(size_t)row * nt + tid];
+  } else {
+#pragma unroll
+    for (int e = 0; e < TK_M; ++e) cw[e] = 0u;
+  }
+  const uint32_t wtop = cw[0];   // the tile's largest word
+  const uint32_t lmax = wtop >> 16;
+  // block maxima: the top word (greedy), the top key, the largest non-candidate
+  // key; the smallest tile maximum over the holders
+  {
+    const uint32_t a = __ockl_wfred_max_u32(wtop);
+    const uint32_t b = __ockl_wfred_max_u32(rw >> 16);
+    const uint32_t c = __ockl_wfred_min_u32(tid < holders ? lmax : 0xffffffffu);
+    if (lane == 0) {
+      s_mx[0][wv] = a;
+      s_mx[1][wv] = b;
+      s_mx[2][wv] = c;
+    }
+    s_lmax[tid] = (unsigned short)lmax;
+    if (tid == 0) { s_sel[1] = 0u; s_nf = 0u; }
+  }
+  __syncthreads();
+  uint32_t gtop = 0u, rmax = 0u, lmin = 0xffffffffu;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) {
+    gtop = max(gtop, s_mx[0][w]);
+    rmax = max(rmax, s_mx[1][w]);
+    lmin = min(lmin, s_mx[2][w]);
+  }
+  if (temperature == 0.f) {   // greedy: the tiles' largest words hold the row's
+    if (tid == 0) {
+      out_tok[row] = (int32_t)(0xffffu - (gtop & 0xffffu));
+      if (pos) pos[row] = pos0 + pos_adv;
+    }
+    return;
+  }
+  const uint32_t kmax = gtop >> 16;
+
+  // ---- k-th largest candidate key T (as in sample_keys_row)
+  bool fast = top_k > 0 && top_k < Vs && top_k <= holders;
+  uint32_t thr = 0u;
+  if (fast) {
+    if (wv == 0) {
+      uint32_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = ((const uint32_t*)s_lmax)[j * 64 + lane];
+      const uint32_t lb = wave_kth(v, lmin, kmax, (uint32_t)top_k);
+      if (lane == 0) s_sel[0] = lb;
+    }
+    __syncthreads();
+    const uint32_t lo = s_sel[0];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < TK_M; ++e) cnt += (cw[e] >> 16) >= lo ? 1u : 0u;
+    uint32_t incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    uint32_t wb = 0;
+    if (lane == 63) wb = atomicAdd(&s_sel[1], incl);
+    wb = __shfl(wb, 63, 64);
+    if (cnt) {
+      uint32_t p = wb + incl - cnt;
+#pragma unroll
+      for (int e = 0; e < TK_M; ++e) {
+        const uint32_t k = cw[e] >> 16;
+        if (k >= lo) { if (p < (uint32_t)SMP_CAP) s_list[p] = (unsigned short)k; ++p; }
+      }
+    }
+    __syncthreads();
+    const uint32_t n = s_sel[1];   // >= top_k
+    if (n <= (uint32_t)SMP_CAP) {
+      if (wv == 0) {
+        uint32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t i = (uint32_t)(j * 64 + lane);
+          const uint32_t w = ((const uint32_t*)s_list)[i];
+          v[j] = (2 * i < n ? (w & 0xffffu) : 0u) | (2 * i + 1 < n ? (w & 0xffff0000u) : 0u);
+        }
+        const uint32_t t = wave_kth(v, lo, kmax, (uint32_t)top_k);
+        if (lane == 0) s_sel[0] = t;
+      }
+      __syncthreads();
+      thr = s_sel[0];
+    } else {
+      uint32_t a = lo, b = kmax;
+      int round = 0;
+      while (a < b) {
+        const uint32_t mid = (a + b + 1) >> 1;
+        uint32_t c = 0;
+#pragma unroll
+        for (int e = 0; e < TK_M; ++e) c += (cw[e] >> 16) >= mid ? 1u : 0u;
+        c = (uint32_t)__ockl_wfred_add_i32((int)c);
+        const uint32_t tot = block_sum_waves(c, s_cnt[round++ & 1]);
+        if (tot >= (uint32_t)top_k) a = mid;
+        else b = mid - 1;
+      }
+      thr = a;
+    }
+  }
+  // kept set = keys >= tk (the softcap saturation rule of sample_keys_row)
+  const float tmp = temperature;
+  uint32_t tk = thr > 1u ? thr : 1u;
+  if (fast && thr > 1u) {
+    const float zthr = softcap(key2f(thr)) / tmp;
+    if (softcap(key2f(thr - 1)) / tmp >= zthr) {
+      uint32_t a = 1, b = thr - 1;
+      while (a < b) {
+        const uint32_t mid = (a + b) >> 1;
+        if (softcap(key2f(mid)) / tmp >= zthr) b = mid;
+        else a = mid + 1;
+      }
+      tk = a;
+    }
+  }
+  // verify (a check of the recomputation): every tile with more than TK_M
+  // valid columns is recomputed and its top TK_M + 1 words compared with the
+  // GEMM's; a difference sets bit 1 of *verify
+  fast = fast && rmax < tk && !verify;
+
+  if (fast) {
+    // ---- kept candidates of this thread in column order: (n << 16 | key),
+    // dropped ones ~0
+    uint32_t it[TK_M];
+#pragma unroll
+    for (int e = 0; e < TK_M; ++e)
+      it[e] = (cw[e] >> 16) >= tk ? ((0xffffu - (cw[e] & 0xffffu)) << 16) | (cw[e] >> 16)
+                                  : 0xffffffffu;
+    // Batcher's odd-even merge sort of 8
+    cas(it[0], it[1]); cas(it[2], it[3]); cas(it[4], it[5]); cas(it[6], it[7]);
+    cas(it[0], it[2]); cas(it[1], it[3]); cas(it[4], it[6]); cas(it[5], it[7]);
+    cas(it[1], it[2]); cas(it[5], it[6]);
+    cas(it[0], it[4]); cas(it[1], it[5]); cas(it[2], it[6]); cas(it[3], it[7]);
+    cas(it[2], it[4]); cas(it[3], it[5]);
+    cas(it[1], it[2]); cas(it[3], it[4]); cas(it[5], it[6]);
+    const float c2 = 1.4426950408889634f / tmp;
+    const float scmax = softcap_fast(key2f(kmax));
+    auto wt = [&](uint32_t k) -> float {
+      return __builtin_amdgcn_exp2f((softcap_fast(key2f(k)) - scmax) * c2);
+    };
+    float local = 0.f;
+    int lastk = -1;
+#pragma unroll
+    for (int e = 0; e < TK_M; ++e)
+      if (it[e] != 0xffffffffu) {
+        local += wt(it[e] & 0xffffu);
+        lastk = (int)(it[e] >> 16);
+      }
+    float incl = local;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (lane == 63) s_wsum[wv] = incl;
+    if (tid == 0) { s_misc[0] = 0xffffffffu; s_misc[1] = 0u; }
+    __syncthreads();
+    float wbase = 0.f, total = 0.f;
+#pragma unroll
+    for (int w = 0; w < SMP_THREADS / 64; ++w) {
+      if (w < wv) wbase += s_wsum[w];
+      total += s_wsum[w];
+    }
+    const float before = wbase + incl - local;
+    const uint32_t rwd = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
+                                  (uint32_t)seed, (uint32_t)(seed >> 32));
+    const float target = (float)(rwd >> 8) * (1.0f / 16777216.0f) * total;
+    if (local > 0.f && target >= before && target < before + local) {
+      float run = before;
+      int pick = -1;
+#pragma unroll
+      for (int e = 0; e < TK_M; ++e)
+        if (it[e] != 0xffffffffu) {   // same additions as local
+          run += wt(it[e] & 0xffffu);
+          if (pick < 0 && target < run) pick = (int)(it[e] >> 16);
+        }
+      if (pick < 0) pick = lastk;
+      atomicMin(&s_misc[0], (uint32_t)pick);
+    }
+    if (lastk >= 0) atomicMax(&s_misc[1], (uint32_t)lastk);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t pick = s_misc[0] != 0xffffffffu ? s_misc[0] : s_misc[1];
+      out_tok[row] = (int32_t)pick;
+      if (pos) pos[row] = pos0 + pos_adv;
+      steps[row] = step + 1;
+    }
+    return;
+  }
+
+  // ---- whole row in LDS: candidates of the tiles whose other keys lie below
+  // fl, recomputed keys of the rest
+  const uint32_t fl = thr > 0u && !verify ? tk : 1u;
+  const int nk8 = nt * 16;   // 16-byte chunks of the row
+  for (int i = tid; i < nk8; i += SMP_THREADS) ((uint4*)s_row)[i] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  if (tid < holders) {
+    if ((rw >> 16) >= fl) {
+      s_flag[atomicAdd(&s_nf, 1u)] = (unsigned short)tid;
+    } else {
+#pragma unroll
+      for (int e = 0; e < TK_M; ++e)
+        if (cw[e]) s_row[0xffffu - (cw[e] & 0xffffu)] = (unsigned short)(cw[e] >> 16);
+    }
+  }
+  __syncthreads();
+  const int nf = (int)s_nf;
+  const bf16_t* arow = A + (size_t)row * lda;
+  const bf16x8_t zero8 = {};
+  for (int f = wv; f < nf; f += SMP_THREADS / 64) {
+    const int t = s_flag[f];
+    floatx4_t acc[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    const bf16_t* wr[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+      wr[nb] = W + (size_t)min(t * 128 + nb * 16 + (lane & 15), N - 1) * K + (lane >> 4) * 8;
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8_t a =
+          (lane & 15) == 0 ? *(const bf16x8_t*)(arow + k0 + (lane >> 4) * 8) : zero8;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8_t*)(wr[nb] + k0), a,
+                                                          acc[nb], 0, 0, 0);
+    }
+    // lane (lane & 15) == 0 holds rows n = 4 (lane >> 4) + r of each block
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const int n = t * 128 + nb * 16 + (lane >> 4) * 4;
+        uint32_t kq[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) kq[r] = n + r < Vs ? zkey(f2bf(acc[nb][r])) : 0u;
+        *(uint2*)(s_row + n) = make_uint2(kq[0] | (kq[1] << 16), kq[2] | (kq[3] << 16));
+      }
+    }
+  }
+  __syncthreads();
+  if (verify && tid < holders && (rw >> 16) >= fl) {
+    // the recomputed tile's TK_M + 1 largest words are the GEMM's
+    bool ok = s_row[0xffffu - (rw & 0xffffu)] == (rw >> 16);
+#pragma unroll
+    for (int e = 0; e < TK_M; ++e)
+      ok = ok && cw[e] != 0u && s_row[0xffffu - (cw[e] & 0xffffu)] == (cw[e] >> 16);
+    uint32_t above = 0;
+    for (int j = 0; j < 128; ++j) {
+      const int n = tid * 128 + j;
+      if (n < Vs) above += (((uint32_t)s_row[n] << 16) | (0xffffu - (uint32_t)n)) > rw ? 1u : 0u;
+    }
+    if (!ok || above != (uint32_t)TK_M) atomicOr(verify, 2u);
+  }
+  const int base = tid * SMP_PER;
+  const int nvalid = max(0, min(SMP_PER, Vs - base));
+  uint32_t kk[SMP_PER / 2];
+#pragma unroll
+  for (int c = 0; c < SMP_CH; ++c) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (c * 8 < nvalid) v = *(const uint4*)(s_row + base + c * 8);
+    kk[4 * c + 0] = v.x;
+    kk[4 * c + 1] = v.y;
+    kk[4 * c + 2] = v.z;
+    kk[4 * c + 3] = v.w;
+  }
+  sample_keys_row(kk, Vs, row, temperature, top_k, seed, step, pos0, steps, out_tok, pos,
+                  pos_adv);
+}
+
 __global__ void k_set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
                                int top_k, unsigned long long seed, unsigned long long step) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -404,6 +751,24 @@ hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_sample, dim3(B), dim3(SMP_THREADS), 0, st, z, ldz, Vs, sp, steps, out_tok,
                      pos, pos_adv);
+  return hipGetLastError();
+}
+
+hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int B, int Vs,
+                       const bf16_t* A, int lda, const bf16_t* W, int N, int K,
+                       const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
+                       int32_t* pos, int pos_adv, unsigned* verify, hipStream_t st) {
+  if (Vs < 1 || Vs > N || nt != (N + 127) / 128 || nt > SMP_THREADS || Vs > SMP_THREADS * SMP_PER ||
+      K % 32 || K < 32 || lda % 8 || ((uintptr_t)A & 15) || ((uintptr_t)W & 15) ||
+      ((uintptr_t)cand & 15))
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)nt * 128 * 2;
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)k_sample_cand, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+  if (attr != hipSuccess) return attr;
+  if (lds > 128 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_sample_cand, dim3(B), dim3(SMP_THREADS), lds, st, cand, cand_r, nt, Vs, A,
+                     lda, W, N, K, sp, steps, out_tok, pos, pos_adv, verify);
   return hipGetLastError();
 }
 

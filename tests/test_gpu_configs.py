@@ -93,8 +93,9 @@ def test_cfg3_shape_b64_prefill512_topk50():
     assert draws == 64 * 4
 
 
+@pytest.mark.parametrize("cand", [True, False], ids=["candidates", "z"])
 @pytest.mark.parametrize("case", ["period600", "levels"])
-def test_sampler_tied_logits_full_vocab(case):
+def test_sampler_tied_logits_full_vocab(case, cand, monkeypatch):
     """The top-k sampler over the real vocabulary with tied logits (k = 50,
     T = 0.8).  period600: lm_head columns repeat with period 600, so each
     logit value has ~84 copies, at most one per thread's 56 entries; the top
@@ -102,7 +103,11 @@ def test_sampler_tied_logits_full_vocab(case):
     column is one of three multiples of one vector (30, 2000 and the rest of
     the columns), so 2030 or ~48,000 keys reach the per-thread-maxima bound
     and the sampler falls back to its block-wide bisection from that bound.
-    Draws against the oracle sampler on the engine's own logits."""
+    Both sampler inputs: the lm_head's top-k candidates (levels: every tile
+    holds more tied keys than its 8 candidates, so each row is recomputed) and
+    z (ANN_TOPK_CAND=0).  Draws against the oracle sampler on the engine's own
+    logits."""
+    monkeypatch.setenv("ANN_TOPK_CAND", "1" if cand else "0")
     cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
                     long_layers=(1,))
     p = perturb_lambdas(init_params(cfg, 61, dense=True))
@@ -152,6 +157,59 @@ def _draw_position(got, z, temp, k, u):
     if j >= keep.size or keep[j] != got or abs(j - i) != 1:
         return None
     return 1 if abs(c[min(i, j)] - t) <= 1e-5 * c[-1] else None
+
+
+@pytest.mark.parametrize("B", [16, 80])
+def test_topk_candidates_recompute_bitwise(B, monkeypatch):
+    """The candidate sampler's recomputation of lm_head tiles is bit-identical
+    to the GEMM: with ANN_TOPK_VERIFY=1 every tile of every row is recomputed
+    and its 9 largest (key, column) words compared with the GEMM epilogue's
+    (a difference fails check_device), and the draws -- now made over the
+    recomputed rows -- equal the oracle sampler's on the engine's logits.
+    16 rows run the 64-row lm_head tiles, 80 rows the 128-row ones."""
+    monkeypatch.setenv("ANN_TOPK_VERIFY", "1")
+    cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 67, dense=True))
+    p["lm_head"] = p["lm_head"] * 4
+    print(f"case candidate recompute check: d256 L2 V50304 B={B}, T=0.8 top-k 50", flush=True)
+    worst, draws = _run_case(cfg, p, B, 12, 3, [0, B - 1], 0.8, 50, 31, 64)
+    assert worst < LOGIT_TOL, worst
+    assert draws == B * 3
+
+
+def test_topk_candidates_clustered_tile_falls_back():
+    """Top keys clustered in one lm_head tile: columns 1000-1039 (tile 7)
+    are pairs +-12 u_j, so every row has 11-19 of its 50 largest logits in
+    that tile (oracle logits), more than its 8 candidates; the sampler
+    recomputes that tile (the other tiles' keys beyond their candidates lie
+    below the threshold) and draws over the whole row.  The check repeats at
+    top-k 200, and at top-k 5, where the tile's candidates hold its 4-5 kept
+    keys and the sampler stays on the candidates.  Draws against the oracle
+    sampler on the engine's logits."""
+    cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 68, dense=True))
+    h = p["lm_head"] * 2
+    # columns 1000 + 2j and 1001 + 2j are +-12 u_j: one of each pair is large
+    # and positive for any row
+    u = h[:, 1000:1020].copy()
+    h[:, 1000:1040:2] = 12 * u
+    h[:, 1001:1040:2] = -12 * u
+    p["lm_head"] = np.ascontiguousarray(h)
+    print("case clustered tile: d256 L2 V50304 B=8", flush=True)
+    B, T0 = 8, 12
+    tok = np.random.default_rng(69).integers(0, 50257, (B, T0 + 2))
+    eng = _engine(cfg, p, B, 64, B * T0)
+    for k in (50, 5, 200):
+        nxt, lg = eng.prefill(tok[:, :T0], 0.8, k, seed=41, step=k, want_logits=True)
+        top = lg[:, :50257].topk(k, dim=-1).indices.cpu().numpy()
+        assert ((top >= 1000) & (top < 1040)).sum(axis=1).min() >= min(k - 1, 9), k
+        _check_draws(nxt, lg, 0.8, k, 41, k, cfg.vocab_size)
+        nxt, lg = eng.decode(torch.from_numpy(tok[:, T0].astype(np.int32)).cuda(), 0.8, k,
+                             seed=41, step=k + 1, want_logits=True)
+        _check_draws(nxt, lg, 0.8, k, 41, k + 1, cfg.vocab_size)
+    eng.check_device()
 
 
 def test_cfg4_shape_ctx8192_b16():
