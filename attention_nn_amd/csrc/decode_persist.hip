@@ -43,6 +43,7 @@ constexpr int PD_T = 512;
 constexpr int PD_NW = PD_T / 64;
 constexpr int PD_SLOTS = 12;                 // 16-byte weight chunks per lane in flight
 constexpr int PD_RMAX = PD_NW * PD_SLOTS;    // projection rows per work-group (U = 1)
+extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
 constexpr int PD_KW = 16;                    // keys per wave chunk
 constexpr uint32_t PD_PH = 256;              // tags per step
 
@@ -596,6 +597,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   u64 best[BM];
 #pragma unroll
   for (int b = 0; b < BM; ++b) best[b] = 0ull;
+  // sampled with candidates: this work-group's z (BM x nrow, nrow <= 4d and
+  // <= 64 PD_ZE, host-checked) kept in the free h buffer
+  bf16_t* zsl = ghb;
   auto hdot = [&](int k, const uint4* w) {
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr) {
@@ -624,6 +628,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
             best[b] = key > best[b] ? key : best[b];
           } else if (lane == 0) {
             P.z[(size_t)b * P.V + n] = zb;
+            if (P.cand) zsl[b * nrow + r] = zb;
           }
           if (P.logits && lane == 0) P.logits[(size_t)b * P.V + n] = softcap(bf2f(zb));
         }
@@ -645,6 +650,35 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     hdot(k + 1, wb);
   }
 
+  if (!P.greedy && P.cand) {
+    // candidates of this work-group's slice (sample_cand): wave b < BM takes
+    // row b, lane l the entries l + 64 i; TK_M + 1 rounds of a wave maximum
+    // over the lanes' largest words, each popped from its lane
+    __syncthreads();
+    if (wv < BM) {
+      const int b = wv;
+      uint32_t w[PD_ZE];
+#pragma unroll
+      for (int i = 0; i < PD_ZE; ++i) {
+        const int r = lane + 64 * i, n = r0 + r;
+        w[i] = r < nrow && n < P.Vs
+                   ? (zkey(zsl[b * nrow + r]) << 16) | (0xffffu - (uint32_t)n) : 0u;
+      }
+      uint32_t mine = 0u;   // lane e < TK_M: candidate e; lane TK_M: the next word
+#pragma unroll 1
+      for (int e = 0; e <= TK_M; ++e) {
+        uint32_t lm = w[0];
+#pragma unroll
+        for (int i = 1; i < PD_ZE; ++i) lm = max(lm, w[i]);
+        const uint32_t gm = __ockl_wfred_max_u32(lm);
+        if (lane == e) mine = gm;
+#pragma unroll
+        for (int i = 0; i < PD_ZE; ++i) w[i] = w[i] == gm ? 0u : w[i];
+      }
+      if (lane < TK_M) P.cand[((size_t)b * G + g) * TK_M + lane] = mine;
+      else if (lane == TK_M) P.cand_r[(size_t)b * G + g] = mine;
+    }
+  }
   if (P.greedy) {
     if (lane == 0) {
 #pragma unroll

@@ -74,7 +74,8 @@ WLayout weight_layout(const ann_config& c) {
 }
 
 struct SLayout {  // byte offsets into the workspace
-  size_t pos, sp, steps, amax, acnt, pfsink, x, x0, qkv, q, ao, hn, hid, part, zb, pd, pd_bytes,
+  size_t pos, sp, steps, amax, acnt, pfsink, x, x0, qkv, q, ao, hn, hid, part, zb, pcand, pd,
+      pd_bytes,
       ce, ce_tz, ce_rows, ce_mean, total;
 };
 
@@ -133,6 +134,8 @@ SLayout ws_layout(const ann_config& c) {
   s.ce_tz = off; off += up(M * 4);
   s.ce_rows = off; off += up(M * 4);
   s.ce_mean = off; off += up(4);
+  // the persistent step's top-k candidates (sampled rows)
+  s.pcand = off; off += up((size_t)PD_MAX_B * PD_MAX_G * (TK_M + 1) * 4);
   s.total = off;
   return s;
 }
@@ -516,8 +519,9 @@ int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, flo
                   x + (size_t)(T - 1) * g.d, T * g.d, B, g.V, g.d, ez, st);
     if (rc) return rc;
     // the GEMM's A operand: the rows normalised into hn by proj()
-    HIPCHK(sample_cand(cand, cand_r, nt, B, g.V_sample, c->sp<bf16_t>(c->sl.hn), g.d,
-                       c->wptr(c->wl.head), g.V, g.d, c->sp<SampParams>(c->sl.sp),
+    HIPCHK(sample_cand(cand, cand_r, nt, (g.V_sample + 127) / 128, B, g.V_sample, nullptr,
+                       c->sp<bf16_t>(c->sl.hn), g.d, c->wptr(c->wl.head), g.V, g.d,
+                       c->sp<SampParams>(c->sl.sp),
                        c->sp<unsigned long long>(c->sl.steps), out_tok, pos, pos_adv,
                        c->cand_verify ? dec_err_word(c) : nullptr, st));
     return ANN_OK;
@@ -656,6 +660,14 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.out_tok = out_tok;
   P.pos = c->sp<int32_t>(c->sl.pos);
   P.z = c->sp<bf16_t>(c->sl.zb);
+  // sampled: the step also leaves each work-group's top-k candidates, the
+  // sampler reads z only when they cannot prove the kept set
+  const int G = c->pd_g, zrows = (g.V + G - 1) / G;
+  const bool cands = !greedy && c->cand_env && zrows <= 64 * PD_ZE && zrows <= 4 * g.d;
+  if (cands) {
+    P.cand = c->sp<uint32_t>(c->sl.pcand);
+    P.cand_r = P.cand + (size_t)PD_MAX_B * PD_MAX_G * TK_M;
+  }
   P.logits = logits;
   uint8_t* pd = c->ws + c->sl.pd;
   P.xq = (u64*)(pd + pd_layout(g, 1));
@@ -688,10 +700,19 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
     ProfScope ps(c, ANN_PROF_STEP, st);
     HIPCHK(decode_persist(P, B, c->Dh, c->pd_g, c->pd_coop, st));
   }
-  if (!greedy)
+  if (cands) {
+    int holders = 0;   // work-groups whose rows start below Vs
+    while (holders < G && (long long)g.V * holders / G < g.V_sample) ++holders;
+    // the tiles' records are (row, work-group): row stride G
+    HIPCHK(sample_cand(P.cand, P.cand_r, G, holders, B, g.V_sample, P.z, nullptr, 0, nullptr,
+                       g.V, g.d, c->sp<SampParams>(c->sl.sp),
+                       c->sp<unsigned long long>(c->sl.steps), out_tok, c->sp<int32_t>(c->sl.pos),
+                       1, nullptr, st));
+  } else if (!greedy) {
     HIPCHK(sample(c->sp<bf16_t>(c->sl.zb), g.V, B, g.V_sample, c->sp<SampParams>(c->sl.sp),
                   c->sp<unsigned long long>(c->sl.steps), out_tok, c->sp<int32_t>(c->sl.pos), 1,
                   st));
+  }
   return ANN_OK;
 }
 

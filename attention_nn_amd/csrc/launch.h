@@ -205,17 +205,20 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
 hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
                   unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
                   hipStream_t st);
-// The same draw from the lm_head's EPI_TOPK candidates (cand, cand_r: B rows of
-// nt tiles) instead of z.  Where the candidates cannot prove the kept set
-// complete (ties or clusters beyond TK_M keys in a tile, top_k 0 or above the
-// candidates) the work-group recomputes the tiles concerned from A (the
-// lm_head's normalised input rows, lda) and W (N x K) with the GEMM's MFMA
-// sequence, bit-identical z, and samples over the whole row.  verify (null
-// normally): recompute every tile and set bit 1 of *verify where a tile's
-// top TK_M + 1 words differ from the candidates.
-hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int B, int Vs,
-                       const bf16_t* A, int lda, const bf16_t* W, int N, int K,
-                       const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
+// The same draw from top-k candidates instead of z: B rows of nt tiles
+// (holders of them with valid columns), per tile its TK_M largest words
+// (zkey << 16 | 0xffff - n) in cand (B, nt, TK_M) and its next word in
+// cand_r (B, nt).  Where the candidates cannot prove the kept set complete
+// (ties or clusters beyond TK_M keys in a tile, top_k 0 or above the tiles)
+// the row is sampled whole: from z (B, N) when the producer stored it (the
+// persistent step), else from the 128-column lm_head tiles concerned,
+// recomputed from A (the lm_head's normalised input rows, lda) and W (N x K)
+// with the GEMM's MFMA sequence (bit-identical z).  verify (null normally,
+// recompute form only): recompute every tile and set bit 1 of *verify where
+// a tile's top TK_M + 1 words differ from the candidates.
+hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int holders, int B,
+                       int Vs, const bf16_t* z, const bf16_t* A, int lda, const bf16_t* W, int N,
+                       int K, const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
                        int32_t* pos, int pos_adv, unsigned* verify, hipStream_t st);
 hipError_t set_sampling(SampParams* sp, unsigned long long* steps, int B, float temperature,
                         int top_k, unsigned long long seed, unsigned long long step,
@@ -258,6 +261,12 @@ struct PDParams {
   int p_stride;           // xp: PD_REP_P copies, work-group g reads copy g % PD_REP_P
   int on;                 // work-groups holding the o rows (at most, after the attention ones)
   float scale, shift, eps;
+  // !greedy (or null): per row and work-group the TK_M largest words of its
+  // z slice and the next one (sample_cand's tiles: the G row slices).  Last
+  // in the struct: placed after z they moved the fields behind them and the
+  // 155M batch-1 greedy step measured 1.1% slower
+  uint32_t* cand;
+  uint32_t* cand_r;
 };
 constexpr int PD_MAX_REP = 8;
 // Copies of the h and attention-partial exchanges (their areas hold up to
@@ -267,6 +276,9 @@ constexpr int PD_MAX_REP = 8;
 // copies chosen at run time measured 6% slower (loops and modulo in the step).
 constexpr int PD_REP_H = 4, PD_REP_P = 4;
 constexpr int PD_MAX_B = 4;                       // rows of the persistent step
+// lm_head rows per lane of the persistent step's top-k candidates: a
+// work-group's vocabulary slice of at most 64 PD_ZE rows
+constexpr int PD_ZE = 8;
 constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffers + partials)
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);

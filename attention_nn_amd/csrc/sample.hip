@@ -424,8 +424,9 @@ __device__ __forceinline__ void cas(uint32_t& a, uint32_t& b) {
 }
 
 __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
-    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_r, int nt, int Vs,
-    const bf16_t* __restrict__ A, int lda, const bf16_t* __restrict__ W, int N, int K,
+    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_r, int nt, int holders,
+    int Vs, const bf16_t* __restrict__ zfb, const bf16_t* __restrict__ A, int lda,
+    const bf16_t* __restrict__ W, int N, int K,
     const SampParams* __restrict__ sp, unsigned long long* __restrict__ steps,
     int32_t* __restrict__ out_tok, int32_t* __restrict__ pos, int pos_adv,
     unsigned* __restrict__ verify) {
@@ -445,8 +446,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int32_t pos0 = pos ? pos[row] : 0;
   const uint64_t step = steps[row];
-  const int holders = (Vs + 127) / 128;   // tiles with valid columns
-  uint32_t cw[TK_M], rw = 0u;
+  uint32_t cw[TK_M], rw = 0u;   // holders: the tiles with valid columns
   if (tid < holders) {
     const uint4* src = (const uint4*)(cand + ((size_t)row * nt + tid) * TK_M);
     const uint4 a = src[0], b = src[1];
@@ -645,6 +645,30 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
     return;
   }
 
+  if (zfb) {   // the producer also stored z: k_sample's draw on it
+    const bf16_t* z = zfb + (size_t)row * N;
+    const int base = tid * SMP_PER;
+    const int nvalid = max(0, min(SMP_PER, Vs - base));
+    uint32_t kk[SMP_PER / 2];
+#pragma unroll
+    for (int c = 0; c < SMP_CH; ++c) {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (c * 8 < nvalid) v = *(const uint4*)(z + base + c * 8);
+      kk[4 * c + 0] = okey2(v.x);
+      kk[4 * c + 1] = okey2(v.y);
+      kk[4 * c + 2] = okey2(v.z);
+      kk[4 * c + 3] = okey2(v.w);
+    }
+    if (nvalid < SMP_PER) {
+#pragma unroll
+      for (int j = 0; j < SMP_PER / 2; ++j)
+        kk[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
+    }
+    sample_keys_row(kk, Vs, row, temperature, top_k, seed, step, pos0, steps, out_tok, pos,
+                    pos_adv);
+    return;
+  }
+
   // ---- whole row in LDS: candidates of the tiles whose other keys lie below
   // fl, recomputed keys of the rest
   const uint32_t fl = thr > 0u && !verify ? tk : 1u;
@@ -754,21 +778,28 @@ hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
   return hipGetLastError();
 }
 
-hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int B, int Vs,
-                       const bf16_t* A, int lda, const bf16_t* W, int N, int K,
-                       const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
+hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int holders, int B,
+                       int Vs, const bf16_t* z, const bf16_t* A, int lda, const bf16_t* W, int N,
+                       int K, const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
                        int32_t* pos, int pos_adv, unsigned* verify, hipStream_t st) {
-  if (Vs < 1 || Vs > N || nt != (N + 127) / 128 || nt > SMP_THREADS || Vs > SMP_THREADS * SMP_PER ||
-      K % 32 || K < 32 || lda % 8 || ((uintptr_t)A & 15) || ((uintptr_t)W & 15) ||
-      ((uintptr_t)cand & 15))
+  if (Vs < 1 || Vs > N || N > 65536 || holders < 1 || holders > nt || nt > SMP_THREADS ||
+      Vs > SMP_THREADS * SMP_PER || ((uintptr_t)cand & 15))
     return hipErrorInvalidValue;
-  const size_t lds = (size_t)nt * 128 * 2;
-  static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)k_sample_cand, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-  if (attr != hipSuccess) return attr;
-  if (lds > 128 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_sample_cand, dim3(B), dim3(SMP_THREADS), lds, st, cand, cand_r, nt, Vs, A,
-                     lda, W, N, K, sp, steps, out_tok, pos, pos_adv, verify);
+  size_t lds = 0;
+  if (z) {   // fallback from z (B, N)
+    if (N % 8 || ((uintptr_t)z & 15) || verify) return hipErrorInvalidValue;
+  } else {   // fallback recomputing the GEMM's 128-column tiles
+    if (nt != (N + 127) / 128 || holders != (Vs + 127) / 128 || K % 32 || K < 32 || lda % 8 ||
+        ((uintptr_t)A & 15) || ((uintptr_t)W & 15))
+      return hipErrorInvalidValue;
+    lds = (size_t)nt * 128 * 2;
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)k_sample_cand, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (lds > 128 * 1024) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(k_sample_cand, dim3(B), dim3(SMP_THREADS), lds, st, cand, cand_r, nt,
+                     holders, Vs, z, A, lda, W, N, K, sp, steps, out_tok, pos, pos_adv, verify);
   return hipGetLastError();
 }
 

@@ -93,9 +93,9 @@ def test_cfg3_shape_b64_prefill512_topk50():
     assert draws == 64 * 4
 
 
-@pytest.mark.parametrize("cand", [True, False], ids=["candidates", "z"])
+@pytest.mark.parametrize("route", ["candidates", "z", "persistent"])
 @pytest.mark.parametrize("case", ["period600", "levels"])
-def test_sampler_tied_logits_full_vocab(case, cand, monkeypatch):
+def test_sampler_tied_logits_full_vocab(case, route, monkeypatch):
     """The top-k sampler over the real vocabulary with tied logits (k = 50,
     T = 0.8).  period600: lm_head columns repeat with period 600, so each
     logit value has ~84 copies, at most one per thread's 56 entries; the top
@@ -103,11 +103,12 @@ def test_sampler_tied_logits_full_vocab(case, cand, monkeypatch):
     column is one of three multiples of one vector (30, 2000 and the rest of
     the columns), so 2030 or ~48,000 keys reach the per-thread-maxima bound
     and the sampler falls back to its block-wide bisection from that bound.
-    Both sampler inputs: the lm_head's top-k candidates (levels: every tile
-    holds more tied keys than its 8 candidates, so each row is recomputed) and
-    z (ANN_TOPK_CAND=0).  Draws against the oracle sampler on the engine's own
-    logits."""
-    monkeypatch.setenv("ANN_TOPK_CAND", "1" if cand else "0")
+    Each sampler input: the lm_head's top-k candidates at 8 rows (levels:
+    every tile holds more tied keys than its 8 candidates, so each row is
+    recomputed), z (ANN_TOPK_CAND=0), and at 2 rows the persistent step's
+    candidates with its z as the fallback.  Draws against the oracle sampler
+    on the engine's own logits."""
+    monkeypatch.setenv("ANN_TOPK_CAND", "0" if route == "z" else "1")
     cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
                     long_layers=(1,))
     p = perturb_lambdas(init_params(cfg, 61, dense=True))
@@ -121,8 +122,8 @@ def test_sampler_tied_logits_full_vocab(case, cand, monkeypatch):
         level[perm[:30]], level[perm[30:2030]] = 0, 1
         alpha = np.array([3.0, 2.0, 1.0], dtype=np.float32)
         p["lm_head"] = np.ascontiguousarray(h[:, :1] * 40 * alpha[level][None, :])
-    print(f"case sampler ties {case}: d256 L2 V50304 B=8, T=0.8 top-k 50", flush=True)
-    B, T0, temp, k, seed = 8, 16, 0.8, 50, 99
+    B, T0, temp, k, seed = 2 if route == "persistent" else 8, 16, 0.8, 50, 99
+    print(f"case sampler ties {case} {route}: d256 L2 V50304 B={B}, T=0.8 top-k 50", flush=True)
     tok = np.random.default_rng(7).integers(0, 50257, (B, T0 + 3))
     eng = _engine(cfg, p, B, 64, B * T0)
     nxt, lg = eng.prefill(tok[:, :T0], temp, k, seed=seed, step=0, want_logits=True)
@@ -210,6 +211,23 @@ def test_topk_candidates_clustered_tile_falls_back():
                              seed=41, step=k + 1, want_logits=True)
         _check_draws(nxt, lg, 0.8, k, 41, k + 1, cfg.vocab_size)
     eng.check_device()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_persistent_sampled_155m_dims_topk_candidates(B):
+    """Sampled decode (T = 0.8, top-k 50) on the persistent step at the 155M
+    dims (d768 H6 x 128, V = 50304, two layers): each work-group leaves its
+    slice's 8 largest keys and the next one, and the sampler draws from those
+    (z only when they cannot prove the kept set).  Logits against the
+    oracle's KV-cache forward, every draw against the oracle sampler on the
+    engine's logits."""
+    cfg = GPTConfig(num_layers=2, num_heads=6, model_dim=768, seq_len=256, window=64,
+                    long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 73, dense=True))
+    print(f"case persistent sampled 155M dims: L2 B={B}", flush=True)
+    worst, draws = _run_case(cfg, p, B, 16, 8, list(range(B)), 0.8, 50, 5, 64)
+    assert worst < LOGIT_TOL, worst
+    assert draws == B * 8
 
 
 def test_cfg4_shape_ctx8192_b16():
