@@ -529,8 +529,8 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
   constexpr int CH = AC > BC ? AC : BC;
   // the QKV and CE epilogues work on 128-column tiles (whole heads; the
   // per-tile partial sums of the loss)
-  static_assert((EPI != EPI_QKV && EPI != EPI_CE && EPI != EPI_TOPK) || BN == GM_BN,
-                "128-column tiles");
+  static_assert((EPI != EPI_QKV && EPI != EPI_CE) || BN == GM_BN, "128-column tiles");
+  static_assert(EPI != EPI_TOPK || BN % 128 == 0, "whole 128-column candidate tiles");
   // staged epilogues (QKV; PE_B / PE_X on full tiles) reuse the LDS for a bf16
   // BM x BN tile of row pitch BN + 8
   // the batched plain store stages its 128 x 128 tiles for the symmetric form
@@ -813,7 +813,11 @@ __device__ __forceinline__ void gemm_body(const bf16_t* __restrict__ A, int lda,
             make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
       }
     __syncthreads();
-    topk_tile_epilogue<BM, CP>(ea, smem, m0, n0, M, N, tn, tid);
+#pragma unroll
+    for (int hf = 0; hf < BN / 128; ++hf)
+      if (tn * (BN / 128) + hf < ea.nt)
+        topk_tile_epilogue<BM, CP>(ea, smem + hf * 128, m0, n0 + hf * 128, M, N,
+                                   tn * (BN / 128) + hf, tid);
   } else {
     if constexpr (EPI == EPI_PE_B || EPI == EPI_PE_X) {
       // full tiles with 16-byte rows: x prefetched before the staging
@@ -1506,13 +1510,14 @@ hipError_t gemm(int epi, const bf16_t* A, int lda, const bf16_t* W, int M, int N
       if (!ea.ce_part || !ea.ce_tz || !ea.tgt || ea.ldz < M) return hipErrorInvalidValue;
       ANN_GM_ONE(EPI_CE, shape)
       break;
-    case EPI_TOPK:
-      // decode rows only (the 64- and 128-row tiles); every column tile one record
-      if (shape > 1 || !ea.cand || !ea.cand_r || ea.nt != (int)grid.x || ea.Vs < 1 ||
+    case EPI_TOPK: {
+      // decode rows only (the 64- and 128-row tiles); every 128 columns one record
+      if (shape > 1 || !ea.cand || !ea.cand_r || ea.nt != (N + 127) / 128 || ea.Vs < 1 ||
           ea.Vs > N || N > 65536 || (ea.logits && ea.ldz < N))
         return hipErrorInvalidValue;
       ANN_GM_ONE(EPI_TOPK, shape)
       break;
+    }
     default:
       return hipErrorInvalidValue;
   }
