@@ -436,8 +436,8 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
   __shared__ float s_wsum[SMP_THREADS / 64];
   __shared__ uint32_t s_misc[2];
   __shared__ __attribute__((aligned(16))) unsigned short s_lmax[SMP_THREADS];
-  __shared__ __attribute__((aligned(16))) unsigned short s_list[SMP_CAP];
-  __shared__ uint32_t s_sel[2];
+  __shared__ uint32_t s_item[SMP_CAP];   // listed candidates: n << 16 | key
+  __shared__ uint32_t s_sel[3];   // [0] bound / threshold, [1] list length, [2] see below
   __shared__ uint32_t s_nf;
   __shared__ unsigned short s_flag[SMP_THREADS];
   const float temperature = sp->temperature;
@@ -494,12 +494,16 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
   bool fast = top_k > 0 && top_k < Vs && top_k <= holders;
   uint32_t thr = 0u;
   if (fast) {
-    if (wv == 0) {
+    if (wv == 0) {   // (a ballot count per 64 maxima measured slower: 2.6 against 1.8 us)
       uint32_t v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = ((const uint32_t*)s_lmax)[j * 64 + lane];
       const uint32_t lb = wave_kth(v, lmin, kmax, (uint32_t)top_k);
-      if (lane == 0) s_sel[0] = lb;
+      if (lane == 0) {
+        s_sel[0] = lb;
+        // 1: no key below lb rounds to the softcapped value of lb (tk >= lb)
+        s_sel[2] = softcap(key2f(lb - 1)) / temperature < softcap(key2f(lb)) / temperature;
+      }
     }
     __syncthreads();
     const uint32_t lo = s_sel[0];
@@ -520,19 +524,87 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample_cand(
 #pragma unroll
       for (int e = 0; e < TK_M; ++e) {
         const uint32_t k = cw[e] >> 16;
-        if (k >= lo) { if (p < (uint32_t)SMP_CAP) s_list[p] = (unsigned short)k; ++p; }
+        if (k >= lo) {
+          if (p < (uint32_t)SMP_CAP) s_item[p] = ((0xffffu - (cw[e] & 0xffffu)) << 16) | k;
+          ++p;
+        }
       }
     }
     __syncthreads();
     const uint32_t n = s_sel[1];   // >= top_k
+    // At most 64 listed keys, every non-candidate key below lo, and no key
+    // below lo rounding to the softcapped value of lo (so tk >= lo and the
+    // kept set lies in the list): wave 0 finishes alone, one item per lane.
+    if (n <= 64u && rmax < lo && !verify && s_sel[2]) {
+      if (wv != 0) return;
+      const uint32_t it = lane < (int)n ? s_item[lane] : 0u;
+      const uint32_t key = it & 0xffffu;
+      uint32_t a = lo, b = kmax;   // T: the top_k-th largest listed key
+      while (a < b) {
+        const uint32_t mid = (a + b + 1) >> 1;
+        if ((uint32_t)__builtin_popcountll(__ballot(key >= mid)) >= (uint32_t)top_k) a = mid;
+        else b = mid - 1;
+      }
+      const uint32_t t1 = a;
+      uint32_t tq = t1;   // tk in [lo, T] (the softcap saturation rule)
+      const float zthr = softcap(key2f(t1)) / temperature;
+      if (t1 > lo && softcap(key2f(t1 - 1)) / temperature >= zthr) {
+        uint32_t c = lo, e = t1 - 1;
+        while (c < e) {
+          const uint32_t mid = (c + e) >> 1;
+          if (softcap(key2f(mid)) / temperature >= zthr) e = mid;
+          else c = mid + 1;
+        }
+        tq = c;
+      }
+      // kept items in column order: a bitonic sort of (n << 16 | key) over
+      // the lanes, dropped ones ~0 (last)
+      uint32_t sv = key >= tq && lane < (int)n ? it : 0xffffffffu;
+#pragma unroll
+      for (int kk = 2; kk <= 64; kk <<= 1)
+#pragma unroll
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+          const uint32_t o = (uint32_t)__shfl_xor((int)sv, jj, 64);
+          const bool asc = (lane & kk) == 0, low = (lane & jj) == 0;
+          sv = (asc == low) ? min(sv, o) : max(sv, o);
+        }
+      const int nk = __builtin_popcountll(__ballot(sv != 0xffffffffu));
+      const float c2 = 1.4426950408889634f / temperature;
+      const float scmax = softcap_fast(key2f(kmax));
+      const float w = lane < nk ? __builtin_amdgcn_exp2f(
+                                      (softcap_fast(key2f(sv & 0xffffu)) - scmax) * c2)
+                                : 0.f;
+      float incl = w;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float x = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += x;
+      }
+      const float total = __shfl(incl, 63, 64);
+      const uint32_t rwd = philox_x((uint32_t)step, (uint32_t)row, (uint32_t)(step >> 32), 0u,
+                                    (uint32_t)seed, (uint32_t)(seed >> 32));
+      const float target = (float)(rwd >> 8) * (1.0f / 16777216.0f) * total;
+      // the first item whose running sum exceeds the target; rounding can
+      // leave the target at or past the last: then the last kept item
+      const uint64_t hit = __ballot(lane < nk && target < incl);
+      const int src = hit ? __builtin_ctzll(hit) : nk - 1;
+      const uint32_t tok = (uint32_t)__shfl((int)sv, src, 64) >> 16;
+      if (lane == 0) {
+        out_tok[row] = (int32_t)tok;
+        if (pos) pos[row] = pos0 + pos_adv;
+        steps[row] = step + 1;
+      }
+      return;
+    }
     if (n <= (uint32_t)SMP_CAP) {
-      if (wv == 0) {
+      if (wv == 0) {   // keys of items 2i and 2i + 1, i = 64 j + lane
         uint32_t v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const uint32_t i = (uint32_t)(j * 64 + lane);
-          const uint32_t w = ((const uint32_t*)s_list)[i];
-          v[j] = (2 * i < n ? (w & 0xffffu) : 0u) | (2 * i + 1 < n ? (w & 0xffff0000u) : 0u);
+          const uint32_t k0 = 2 * i < n ? (s_item[2 * i] & 0xffffu) : 0u;
+          const uint32_t k1 = 2 * i + 1 < n ? (s_item[2 * i + 1] & 0xffffu) : 0u;
+          v[j] = k0 | (k1 << 16);
         }
         const uint32_t t = wave_kth(v, lo, kmax, (uint32_t)top_k);
         if (lane == 0) s_sel[0] = t;
