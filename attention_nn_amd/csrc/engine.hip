@@ -514,6 +514,7 @@ int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, flo
     ez.cand = cand;
     ez.cand_r = cand_r;
     ez.nt = nt;
+    ez.tk_first = greedy ? 1 : 0;
     ez.Vs = g.V_sample;
     int rc = proj(c, ANN_PROF_LM_HEAD, EPI_TOPK, PRE_RMS, c->wptr(c->wl.head),
                   x + (size_t)(T - 1) * g.d, T * g.d, B, g.V, g.d, ez, st);

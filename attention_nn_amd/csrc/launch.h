@@ -53,10 +53,11 @@ struct EpiArgs {
   // amax[m * blocks + block]; argmax_finalize turns them into tokens.
   unsigned long long* amax;
   int Vs;
-  // TOPK: candidate words (M, nt, TK_M) and 9th-largest words (M, nt)
+  // TOPK: candidate words (M, nt, TK_M) and 9th-largest words (M, nt);
+  // tk_first: greedy rows, only each tile's largest word (cand[.. * TK_M])
   uint32_t* cand;
   uint32_t* cand_r;
-  int nt;
+  int nt, tk_first;
   // QKV: row m = b * T + t; model dim d = H * Dh; caches [B][H][max_ctx][Dh]
   bf16_t* kc;
   bf16_t* vc;

@@ -455,6 +455,7 @@ __device__ __forceinline__ void topk_tile_epilogue(const EpiArgs& ea, const bf16
               lr[e] = softcap(__uint_as_float(e & 1 ? hw[e >> 1] & 0xffff0000u : hw[e >> 1] << 16));
         }
       }
+      if (ea.tk_first) continue;   // greedy: the maximum only (below)
       // Batcher's odd-even merge sort of 8, descending
       uint32_t(&x)[8] = w[q];
       cas_desc(x[0], x[1]); cas_desc(x[2], x[3]); cas_desc(x[4], x[5]); cas_desc(x[6], x[7]);
@@ -463,6 +464,18 @@ __device__ __forceinline__ void topk_tile_epilogue(const EpiArgs& ea, const bf16
       cas_desc(x[0], x[4]); cas_desc(x[1], x[5]); cas_desc(x[2], x[6]); cas_desc(x[3], x[7]);
       cas_desc(x[2], x[4]); cas_desc(x[3], x[5]);
       cas_desc(x[1], x[2]); cas_desc(x[3], x[4]); cas_desc(x[5], x[6]);
+    }
+    if (ea.tk_first) {   // greedy rows: each tile's largest word
+#pragma unroll
+      for (int q = 0; q < RP; ++q) {
+        uint32_t lm = w[q][0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) lm = max(lm, w[q][e]);
+        const uint32_t g = row16_max(lm);
+        const int m = m0 + (p + q) * 16 + grp;
+        if (m < M && li == 0) ea.cand[((size_t)m * ea.nt + tn) * TK_M] = g;
+      }
+      continue;
     }
     uint32_t mine[RP];   // lane li < 8: candidate li; lane 8: the 9th word
 #pragma unroll
