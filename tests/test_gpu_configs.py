@@ -179,6 +179,30 @@ def test_topk_candidates_recompute_bitwise(B, monkeypatch):
     assert draws == B * 3
 
 
+@pytest.mark.parametrize("V, B", [(50304, 4), (50304, 70), (40000, 4)])
+def test_topk_candidates_draws_match_oracle_full_vocab(V, B):
+    """Draws over a full vocabulary at the rows the candidate lm_head takes
+    (4: 64-row tiles, 70: 128-row tiles; V = 40000 leaves a last tile of 64
+    columns and samples over every column), for temperatures 0.5 / 0.8 / 2
+    and top_k 1, 2, 5, 50 and 256 (the candidate route's limit), 257 and 0
+    (every entry kept: z), plus greedy: each row's draw equals the oracle
+    sampler's on the engine's logits (Philox counter (step, row))."""
+    cfg = GPTConfig(vocab_size=V, num_layers=2, num_heads=2, model_dim=256, seq_len=64,
+                    window=16, long_layers=(1,))
+    p = perturb_lambdas(init_params(cfg, 74, dense=True))
+    p["lm_head"] = p["lm_head"] * 8
+    print(f"case candidate draws: d256 L2 V{V} B={B}", flush=True)
+    tok = np.random.default_rng(75).integers(0, min(V, 50257), (B, 10))
+    eng = _engine(cfg, p, B, 64, B * 64)
+    cases = [(0.8, 50), (0.5, 1), (2.0, 2), (0.8, 5), (1.0, 256), (0.8, 257), (0.8, 0), (0.0, 0)]
+    for step, (temp, k) in enumerate(cases):
+        nxt, lg = eng.prefill(tok, temp, k, seed=9, step=step, want_logits=True)
+        _check_draws(nxt, lg, temp, k, 9, step, V)
+        nxt, lg = eng.decode(nxt, temp, k, seed=9, step=100 + step, want_logits=True)
+        _check_draws(nxt, lg, temp, k, 9, 100 + step, V)
+    eng.check_device()
+
+
 def test_topk_candidates_clustered_tile_falls_back():
     """Top keys clustered in one lm_head tile: columns 1000-1039 (tile 7)
     are pairs +-12 u_j, so every row has 11-19 of its 50 largest logits in
