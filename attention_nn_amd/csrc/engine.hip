@@ -476,7 +476,9 @@ int check_sampling(const ann_ctx* c, const ann_sampling* s) {
   if (!s) return fail(ANN_E_ARG, "sampling is null");
   if (!(s->temperature >= 0.f) || s->temperature != s->temperature)
     return fail(ANN_E_ARG, "temperature must be >= 0");
-  (void)c;
+  // the samplers read z rows in 16-byte chunks
+  if (s->temperature != 0.f && c->c.V % 8)
+    return fail(ANN_E_ARG, "sampling (temperature > 0) needs V a multiple of 8 (V=%d)", c->c.V);
   return ANN_OK;
 }
 

@@ -84,6 +84,26 @@ def test_sizes(L):
     assert L.ann_weight_bytes(ctypes.byref(bad)) == 0
 
 
+def test_sampling_needs_vocab_multiple_of_8(L):
+    """Sampled calls (temperature > 0) are refused on the host for a vocabulary
+    that is not a multiple of 8 (the samplers read z rows in 16-byte chunks)."""
+    c = _cfg(V=50257, V_sample=50257)
+    rc, ctx = _create(L, c)
+    assert rc == 0
+    try:
+        fake = ctypes.c_void_p(1 << 40)
+        wb = L.ann_weight_bytes(ctypes.byref(c))
+        kb = L.ann_kv_bytes(ctypes.byref(c))
+        sb = L.ann_workspace_bytes(ctypes.byref(c))
+        assert L.ann_bind(ctx, fake, wb, fake, kb, fake, sb) == 0
+        tok = ctypes.c_void_p(0x1000)
+        s = _lib.AnnSampling(0.8, 50, 1, 0)
+        assert L.ann_prefill(ctx, tok, 1, 4, ctypes.byref(s), tok, None, None) == _lib.ANN_E_ARG
+        assert "multiple of 8" in L.ann_last_error().decode()
+    finally:
+        L.ann_destroy(ctx)
+
+
 def test_call_order_and_capacity_errors(L):
     c = _cfg()
     rc, ctx = _create(L, c)
