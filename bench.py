@@ -28,7 +28,9 @@ Every pass ends with the device check of the persistent step's bounded waits
 (a step that gave up would end early and inflate the rate); the run exits
 non-zero if one did.
 
-secondary (each the median of 5 repetitions): batch-64 decode (configs[2]:
+secondary: the same batch-1 generation sampled at sample.py's defaults
+(T = 0.8, top-k 50; median of 3); each of the following the median of 5
+repetitions: batch-64 decode (configs[2]:
 512-token prompts, temperature 0.8, top-k 50) against HBM and its prefill
 against the bf16 MFMA peak; the training forward; one optimizer step;
 configs[3] (B=16 at context 8192) and configs[4] (d1536, B=128).
@@ -436,6 +438,10 @@ def main():
     # events on its stream
     k_ms, k_n = step_kernel_times(eng, prompt, n_decode)
     check(eng, "the roofline generation")
+    # the reference's default sampling (sample.py:18-19: T = 0.8, top-k 50),
+    # same prompt and length: persistent step + top-k candidate sampler
+    s_total, s_gen, s_dec = timed_generations(eng, prompt, n_decode, 3, 1, 0.8, 50, 1)
+    check(eng, "the sampled generations")
     gen_tokens = n_decode + 1
     value = args.steps * gen_tokens / (total_ms / 1e3)
     avg_bytes = float(np.mean([step_bytes(cfg, 1, prompt_len + i) for i in range(n_decode)]))
@@ -477,9 +483,16 @@ def main():
                      "launches": n_decode, "positions": f"{prompt_len}..{prompt_len + n_decode - 1}"},
     }
     step_gbs = avg_bytes / (dec_med / n_decode / 1e3) / 1e9
+    s_dec_med = float(np.median(s_dec))
     sec = {"b1_step": {"avg_alg_bytes": int(avg_bytes), "achieved_GBs": round(step_gbs, 1),
                        "hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                       "generation_ms_reps": [round(x, 3) for x in gen]}}
+                       "generation_ms_reps": [round(x, 3) for x in gen]},
+           "b1_sampled": {"tok_s": round(gen_tokens / (float(np.median(s_gen)) / 1e3), 2),
+                          "decode_ms_per_token": round(s_dec_med / n_decode, 5),
+                          "generation_ms_reps": [round(x, 3) for x in s_gen],
+                          "reps": 3, "statistic": "median",
+                          "workload": "cfg2 shape, batch 1, T = 0.8 / top-k 50 (sample.py "
+                                      "defaults), seed 1, same prompt and length"}}
     del eng
     torch.cuda.empty_cache()
 
