@@ -1028,6 +1028,8 @@ int ann_decode_step(ann_ctx* c, const int32_t* tokens, int32_t B, const ann_samp
   rc = sync_sampling(c, s, B, st);
   if (rc) return rc;
   const bool greedy = s->temperature == 0.f;
+  // set up before the step may be captured into a graph below
+  if (cand_route(c, B, greedy)) HIPCHK(sample_prepare());
   rc = clear_decode_state(c, st);   // tags, tickets, partials and the error word
   if (rc) return rc;
   // The batch-1 persistent step is one kernel (plus the sampler when not

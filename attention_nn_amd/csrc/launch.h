@@ -217,6 +217,9 @@ hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
 // with the GEMM's MFMA sequence (bit-identical z).  verify (null normally,
 // recompute form only): recompute every tile and set bit 1 of *verify where
 // a tile's top TK_M + 1 words differ from the candidates.
+// One-time set-up of the candidate sampler (its dynamic LDS limit), called by
+// the entry points before anything they may capture into a graph.
+hipError_t sample_prepare();
 hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int holders, int B,
                        int Vs, const bf16_t* z, const bf16_t* A, int lda, const bf16_t* W, int N,
                        int K, const SampParams* sp, unsigned long long* steps, int32_t* out_tok,

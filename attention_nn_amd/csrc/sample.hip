@@ -850,6 +850,12 @@ hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
   return hipGetLastError();
 }
 
+hipError_t sample_prepare() {
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)k_sample_cand, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+  return attr;
+}
+
 hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int holders, int B,
                        int Vs, const bf16_t* z, const bf16_t* A, int lda, const bf16_t* W, int N,
                        int K, const SampParams* sp, unsigned long long* steps, int32_t* out_tok,
@@ -865,8 +871,7 @@ hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int
         ((uintptr_t)A & 15) || ((uintptr_t)W & 15))
       return hipErrorInvalidValue;
     lds = (size_t)nt * 128 * 2;
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void*)k_sample_cand, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    const hipError_t attr = sample_prepare();
     if (attr != hipSuccess) return attr;
     if (lds > 128 * 1024) return hipErrorInvalidValue;
   }
