@@ -482,9 +482,6 @@ int check_sampling(const ann_ctx* c, const ann_sampling* s) {
   return ANN_OK;
 }
 
-// z of the last row of each sequence -> sampled token; positions advance by
-// pos_adv (the tokens this call added).  Sampling parameters come from the
-// device copy written by sync_sampling.
 // The device error word: bounded waits that gave up (bit 0), the candidate
 // sampler's check (bit 1).
 unsigned* dec_err_word(ann_ctx* c) { return (unsigned*)(c->ws + c->sl.pd + pd_layout(c->c, 8)); }
@@ -499,6 +496,10 @@ bool cand_route(const ann_ctx* c, int B, bool greedy) {
   return greedy || (c->sp_topk >= 1 && c->sp_topk <= 256 && c->sp_topk < g.V_sample);
 }
 
+// lm_head of the last row of each sequence -> sampled token (from the top-k
+// candidates where cand_route says so, else from z); positions advance by
+// pos_adv (the tokens this call added).  Sampling parameters come from the
+// device copy written by sync_sampling.
 int head_and_sample(ann_ctx* c, int B, int T, bool greedy, int32_t* out_tok, float* logits,
                     int pos_adv, hipStream_t st) {
   const ann_config& g = c->c;

@@ -21,7 +21,7 @@ namespace ann {
 //                   128-column tile t: ce_part[t * ldz + m] = sum of exp(softcap(bf16(y)))
 //                   over the tile's columns; ce_tz[m] = softcap(bf16(y[tgt[m]])) from
 //                   the tile holding the target (metal_kernels.py:153-193)
-//   EPI_TOPK        (MFMA GEMM only, decode lm_head of 3..256 rows) per row m and
+//   EPI_TOPK        (MFMA GEMM only, decode lm_head of 3..511 rows) per row m and
 //                   128-column tile t, over the columns n < Vs: the tile's 8
 //                   largest words (zkey(bf16(y)) << 16 | 0xffff - n, so equal
 //                   keys rank the lower column first) to cand[(m nt + t) 8 ..],
@@ -206,6 +206,9 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
 hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
                   unsigned long long* steps, int32_t* out_tok, int32_t* pos, int pos_adv,
                   hipStream_t st);
+// One-time set-up of the candidate sampler (its dynamic LDS limit), called by
+// the entry points before anything they may capture into a graph.
+hipError_t sample_prepare();
 // The same draw from top-k candidates instead of z: B rows of nt tiles
 // (holders of them with valid columns), per tile its TK_M largest words
 // (zkey << 16 | 0xffff - n) in cand (B, nt, TK_M) and its next word in
@@ -217,9 +220,6 @@ hipError_t sample(const bf16_t* z, int ldz, int B, int Vs, const SampParams* sp,
 // with the GEMM's MFMA sequence (bit-identical z).  verify (null normally,
 // recompute form only): recompute every tile and set bit 1 of *verify where
 // a tile's top TK_M + 1 words differ from the candidates.
-// One-time set-up of the candidate sampler (its dynamic LDS limit), called by
-// the entry points before anything they may capture into a graph.
-hipError_t sample_prepare();
 hipError_t sample_cand(const uint32_t* cand, const uint32_t* cand_r, int nt, int holders, int B,
                        int Vs, const bf16_t* z, const bf16_t* A, int lda, const bf16_t* W, int N,
                        int K, const SampParams* sp, unsigned long long* steps, int32_t* out_tok,

@@ -394,24 +394,30 @@ __global__ __launch_bounds__(SMP_THREADS) void k_sample(const bf16_t* __restrict
 
 // ---- draws from the lm_head's top-k candidates -------------------------------
 //
-// Each 128-column tile t of the lm_head left, per row, its TK_M largest words
-// (key << 16 | 0xffff - n, largest first) and its next largest word r_t
-// (EPI_TOPK).  Thread t holds tile t's candidates.  The k-th largest
-// candidate key T is found like k_sample's threshold (a lower bound from the
-// tile maxima, the keys above it listed and bisected).  If every tile's next
+// Each tile t -- a 128-column tile of the lm_head GEMM (EPI_TOPK), or one
+// work-group's row slice of the persistent step -- left, per row, its TK_M
+// largest words (key << 16 | 0xffff - n, largest first) and its next largest
+// word r_t.  Thread t holds tile t's candidates.  The k-th largest candidate
+// key T is found like k_sample's threshold: a lower bound lb from the tile
+// maxima, then the keys above it listed and bisected.  If every tile's next
 // key r_t lies below the kept threshold tk (<= T), every key >= tk is a
 // candidate: the k-th largest key of the row is T (any larger k-th key would
-// have k candidates above T) and the kept set is the candidates >= tk.
-// Otherwise the tiles with r_t >= tk (all tiles when T could not be formed)
-// are recomputed into an LDS row of keys -- the others contribute their
-// candidates, the rest of their keys lying below tk and below any threshold
-// the full row can give -- and k_sample's whole-row draw runs on that row.
-// The recomputation repeats the lm_head GEMM's accumulation for the row: one
-// v_mfma_f32_16x16x32_bf16 per 32-wide k step in k order, W as the first
-// operand, the row as column 0 of the second, so z is bit-identical.
-// (Measured: the draw from the candidates in one wave, without block
-// barriers, took 14-15 us at 64 rows against 10 us for this form -- one wave
-// issues the counting at a quarter of the CU's VALU rate.)
+// have k candidates above T) and the kept set is the candidates >= tk.  When
+// the list holds at most 64 keys and that is already settled at lb, wave 0
+// finishes alone (ballot-count bisection, a bitonic sort of the kept items
+// into column order across the lanes, a wave scan); otherwise the block
+// draws.  Where the candidates cannot settle it, the row is sampled whole:
+// from z when the producer stored it (the persistent step), else the tiles
+// with r_t >= tk (all tiles when T could not be formed) are recomputed into
+// an LDS row of keys -- the others contribute their candidates, the rest of
+// their keys lying below tk and below any threshold the full row can give --
+// and k_sample's whole-row draw runs on that row.  The recomputation repeats
+// the lm_head GEMM's accumulation for the row: one v_mfma_f32_16x16x32_bf16
+// per 32-wide k step in k order, W as the first operand, the row as column 0
+// of the second, so z is bit-identical.  (Measured: the whole draw in one
+// wave, counting over 64 words per lane, took 14-15 us at 64 rows against
+// 10 us for the block form then -- one wave issues at a quarter of the CU's
+// VALU rate; the single-wave finish above works on one key per lane.)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
