@@ -160,20 +160,21 @@ def _draw_position(got, z, temp, k, u):
     return 1 if abs(c[min(i, j)] - t) <= 1e-5 * c[-1] else None
 
 
-@pytest.mark.parametrize("B", [16, 80])
-def test_topk_candidates_recompute_bitwise(B, monkeypatch):
+@pytest.mark.parametrize("d, H, B", [(256, 2, 16), (256, 2, 80), (768, 6, 64), (1536, 12, 128)])
+def test_topk_candidates_recompute_bitwise(d, H, B, monkeypatch):
     """The candidate sampler's recomputation of lm_head tiles is bit-identical
     to the GEMM: with ANN_TOPK_VERIFY=1 every tile of every row is recomputed
     and its 9 largest (key, column) words compared with the GEMM epilogue's
     (a difference fails check_device), and the draws -- now made over the
     recomputed rows -- equal the oracle sampler's on the engine's logits.
-    16 rows run the 64-row lm_head tiles, 80 rows the 128-row ones."""
+    16 and 64 rows run the 64-row lm_head tiles, 80 and 128 the 128-row ones;
+    K = 256, 768 (cfg3's dims) and 1536 (cfg5's)."""
     monkeypatch.setenv("ANN_TOPK_VERIFY", "1")
-    cfg = GPTConfig(num_layers=2, num_heads=2, model_dim=256, seq_len=128, window=16,
-                    long_layers=(1,))
+    cfg = GPTConfig(num_layers=1 if d > 768 else 2, num_heads=H, model_dim=d, seq_len=128,
+                    window=16, long_layers=(0,) if d > 768 else (1,))
     p = perturb_lambdas(init_params(cfg, 67, dense=True))
     p["lm_head"] = p["lm_head"] * 4
-    print(f"case candidate recompute check: d256 L2 V50304 B={B}, T=0.8 top-k 50", flush=True)
+    print(f"case candidate recompute check: d{d} V50304 B={B}, T=0.8 top-k 50", flush=True)
     worst, draws = _run_case(cfg, p, B, 12, 3, [0, B - 1], 0.8, 50, 31, 64)
     assert worst < LOGIT_TOL, worst
     assert draws == B * 3
