@@ -94,8 +94,7 @@ constexpr int PD_PW = 2;
 
 // Rows of a projection owned by work-group g: pairs [b, e) of npairs, split
 // over the `count` work-groups from `first` on (none for the others).
-__device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr, int first, int count) {
-  const int g = (int)blockIdx.x - first, G = count;
+__device__ __forceinline__ void pd_rows_at(int npairs, int& n0, int& nr, int g, int G) {
   if (g < 0 || g >= G) {
     n0 = nr = 0;
     return;
@@ -103,6 +102,50 @@ __device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr, int first,
   const int b = (int)((long long)npairs * g / G), e = (int)((long long)npairs * (g + 1) / G);
   n0 = 2 * b;
   nr = 2 * (e - b);
+}
+__device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr, int first, int count) {
+  pd_rows_at(npairs, n0, nr, (int)blockIdx.x - first, count);
+}
+
+// qkv rows of work-group g.  With xcd (one row, H <= 8, shares checked by
+// decode_persist_xq_ok) the q, k and v rows of head h come from the
+// work-groups of XCD h (work-group g runs on XCD g % 8), which also run that
+// head's attention splits, so that hand-off stays inside one XCD: the 3 Dh/2
+// row pairs of the head split evenly over the XCD's G / 8 work-groups, each
+// share inside its q, k or v rows.  XCDs numbered H and up hold none.
+// Otherwise the pairs split contiguously over all work-groups.
+template <int P2>
+__device__ __forceinline__ void pd_rows_qkv(int xcd, int H, int d2, int& n0, int& nr) {
+  if (!xcd) {
+    pd_rows(3 * d2, n0, nr, 0, (int)gridDim.x);
+    return;
+  }
+  const int g = (int)blockIdx.x, x = g & 7, i = g >> 3, per = (int)gridDim.x >> 3;
+  if (x >= H) {
+    n0 = nr = 0;
+    return;
+  }
+  const int b = 3 * P2 * i / per, e = 3 * P2 * (i + 1) / per;
+  const int part = b / P2;   // 0 q, 1 k, 2 v
+  n0 = 2 * (part * d2 + x * P2 + (b - part * P2));
+  nr = 2 * (e - b);
+}
+
+// Attention unit (b * H + h) * S + s run by work-group g, or -1.  xcd (one
+// row): unit (h, s) on work-group 8 s + h, i.e. on XCD h with the head's qkv
+// rows; otherwise units 0 .. NA - 1 on work-groups 0 .. NA - 1.
+__device__ __forceinline__ int pd_attn_unit(int xcd, int g, int H, int S, int NA) {
+  if (!xcd) return g < NA ? g : -1;
+  const int x = g & 7, q = g >> 3;
+  return x < H && q < S ? x * S + q : -1;
+}
+
+// Index of work-group g among those without an attention unit (the o rows
+// go to the first of them).
+__device__ __forceinline__ int pd_free_index(int xcd, int g, int H, int S, int NA) {
+  if (!xcd) return g - NA;
+  const int x = g & 7, q = g >> 3;
+  return g - (q < S ? q * H + min(x, H) : S * H);
 }
 
 // Weight chunks of this lane: row n0 + wave + 8 rr (rr < R), chunks
@@ -325,7 +368,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   uint4 wr[PD_SLOTS];
   {
     int n0, nr;
-    pd_rows(3 * d2, n0, nr, 0, G);
+    pd_rows_qkv<P2>(P.head_xcd, H, d2, n0, nr);
     pd_wload2<UD>(P.layers + P.o_qkv, d, n0, nr, wr);
   }
 
@@ -349,7 +392,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     int n0, nr;
 
     // ---- 1: qkv
-    pd_rows(3 * d2, n0, nr, 0, G);
+    pd_rows_qkv<P2>(P.head_xcd, H, d2, n0, nr);
     if (l > 0) pd_wload2<UD>(Wl + P.o_qkv, d, n0, nr, wr);
     if (l > 0) {
       ll_poll(xx_me, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
@@ -361,16 +404,17 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
     // ---- 2: attention of (b, h, split)
     const int S = lng ? P.s_long : P.s_win;
-    const int NA = BM * H * S;   // work-groups 0 .. NA-1 run the attention
-    const bool attn = g < NA;
+    const int NA = BM * H * S;   // attention units (b, h, s)
+    const int au = pd_attn_unit(P.head_xcd, g, H, S, NA);
+    const bool attn = au >= 0;
     // phase 3 (o projection) runs on up to P.on of the other work-groups,
     // whose weights load during the attention; the attention work-groups go
     // on to phase 4 (fewer producers of x' exchange faster: 8 rows each on
     // 96 work-groups measured 1.5% faster per step than 4-6 on 144-174)
-    pd_rows(d2, n0, nr, NA, min(P.on, G - NA));
+    pd_rows_at(d2, n0, nr, attn ? -1 : pd_free_index(P.head_xcd, g, H, S, NA), min(P.on, G - NA));
     if (!attn) pd_wload2<UD>(Wl + P.o_o, d, n0, nr, wr);
     if (attn) {
-      const int s = g % S, h = (g / S) % H, b = g / (S * H);
+      const int s = au % S, h = (au / S) % H, b = au / (S * H);
       const int p = s_pos[b];
       const int lo = lng ? 0 : max(0, p - P.window + 1);
       const int n = p - lo + 1;
@@ -511,7 +555,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       for (int e = 0; e < VD; ++e) s_o[wv][VD * lane + e] = acc[e];
       if (lane == 0) s_l[wv] = lsum;
       __syncthreads();
-      u64* dst = P.xp + (size_t)g * (DH + 1);   // g = (b * H + h) * S + s
+      u64* dst = P.xp + (size_t)au * (DH + 1);
       if (tid < DH) {
         float o = 0.f;
 #pragma unroll
@@ -751,6 +795,21 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
   return true;
 }
 
+// Whether the step can keep each head's qkv rows and attention splits on XCD
+// h: one row, G a multiple of 8 with the S attention splits of a head on
+// work-groups h, h + 8, .., h + 8 (S - 1), at most 8 heads, and the head's
+// 3 Dh/2 row pairs split into equal shares that each stay inside its q, k
+// or v rows and fit a work-group's registers.
+bool decode_persist_xcd_ok(int B, int d, int H, int Dh, int G, int s_long) {
+  if (B != 1 || H < 1 || H > 8 || G < 8 || G % 8 || s_long < 1 || 8 * s_long > G ||
+      H * Dh != d)
+    return false;
+  const int per = G / 8, p2 = Dh / 2;
+  if ((3 * p2) % per) return false;
+  const int q = 3 * p2 / per;
+  return p2 % q == 0 && q <= PD_PW * PD_NW;
+}
+
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
   return (size_t)8 * B * d * 2 + (size_t)B * H * s_long * (Dh + 1) * 4;
 }
@@ -809,6 +868,8 @@ hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hi
   const int rd = 2 * PD_PW * PD_NW;
   const int no = P.on < G - B * P.H * P.s_long ? P.on : G - B * P.H * P.s_long;
   if (no < 1 || 2 * ((P.d / 2 + no - 1) / no) > rd) return hipErrorInvalidValue;
+  if (P.head_xcd && !decode_persist_xcd_ok(B, P.d, P.H, Dh, G, P.s_long))
+    return hipErrorInvalidValue;
   switch (B) {
     case 1: return pd_dispatch<1>(P, Dh, G, lds, coop, st);
     case 2: return pd_dispatch<2>(P, Dh, G, lds, coop, st);

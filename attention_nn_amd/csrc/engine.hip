@@ -231,6 +231,9 @@ struct ann_ctx {
   int pd_max_b = 3;
   int pd_rep = PD_MAX_REP;   // copies of the persistent step's x' / x exchange
   int pd_on = 0;             // work-groups for the o rows (0: d / 8, 8 rows each)
+  // one row: each head's qkv rows and attention splits on one XCD where the
+  // shapes allow (ANN_PD_XCD=0: contiguous over the work-groups)
+  bool pd_xcd_env = true;
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -697,6 +700,7 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.rep_stride = (int)pd_rep_stride(g);
   P.h_stride = (int)pd_h_stride(g);
   P.p_stride = (int)pd_p_stride(g);
+  P.head_xcd = c->pd_xcd_env && decode_persist_xcd_ok(B, g.d, g.H, c->Dh, G, P.s_long) ? 1 : 0;
   P.scale = g.attn_scale;
   P.shift = g.attn_scale * (float)c->Dh * 1.02f;
   P.eps = g.rms_eps;
@@ -777,6 +781,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->pd_env = !(pe && pe[0] == '0');
   const char* on = getenv("ANN_PD_ON");
   c->pd_on = on && atoi(on) > 0 ? atoi(on) : 0;
+  const char* px = getenv("ANN_PD_XCD");
+  c->pd_xcd_env = !(px && px[0] == '0');
   const char* pr = getenv("ANN_PD_REP");
   if (pr && atoi(pr) >= 1 && atoi(pr) <= PD_MAX_REP) c->pd_rep = atoi(pr);
   const char* ds = getenv("ANN_DEC_SPLITS");

@@ -271,6 +271,9 @@ struct PDParams {
   // 155M batch-1 greedy step measured 1.1% slower
   uint32_t* cand;
   uint32_t* cand_r;
+  // one row: each head's qkv rows and attention splits on XCD h (see
+  // decode_persist_xcd_ok), else contiguous over the work-groups
+  int head_xcd;
 };
 constexpr int PD_MAX_REP = 8;
 // Copies of the h and attention-partial exchanges (their areas hold up to
@@ -285,6 +288,7 @@ constexpr int PD_MAX_B = 4;                       // rows of the persistent step
 constexpr int PD_ZE = 8;
 constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffers + partials)
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
+bool decode_persist_xcd_ok(int B, int d, int H, int Dh, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
 hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st);
 

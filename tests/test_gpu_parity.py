@@ -756,6 +756,36 @@ def test_persistent_155m_late_positions_match_oracle():
     assert worst < LOGIT_TOL, worst
 
 
+def test_persistent_155m_head_xcd_layout_bitwise(monkeypatch):
+    """The persistent step's two work layouts at 155M: each head's qkv rows and
+    attention splits on XCD h (the default where the shares divide: 192
+    work-groups, 8 row pairs each) against the rows split contiguously over
+    all work-groups (ANN_PD_XCD=0).  Every row and every attention unit is
+    computed the same way in both, so the logits of a 500-token prefill's
+    decode steps (windowed layers over three splits, full-causal over eight)
+    are bitwise equal, greedy and teacher-forced."""
+    cfg = cfg_155m()
+    p = perturb_lambdas(init_params(cfg, 13, dense=True))
+    tok = np.random.default_rng(131).integers(0, 50257, (1, 520))
+
+    def run(xcd):
+        monkeypatch.setenv("ANN_PD_XCD", xcd)
+        eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+        monkeypatch.delenv("ANN_PD_XCD")
+        print(f"case 155M batch 1, ANN_PD_XCD={xcd}: prefill 500, 20 decode steps", flush=True)
+        eng.prefill(tok[:, :500])
+        lgs = []
+        for i in range(500, 520):
+            t = torch.from_numpy(tok[:, i].astype(np.int32)).cuda()
+            _, lg = eng.decode(t, want_logits=True)
+            lgs.append(lg.cpu())
+        eng.check_device()
+        return torch.stack(lgs)
+
+    a, b = run("1"), run("0")
+    assert torch.equal(a, b), (a - b).abs().max().item()
+
+
 def test_degenerate_init_repeats_last_token():
     """cfg1 as specified (model.py init: Wo = proj = x0 = 0): greedy repeats
     the last prompt token; logits equal the oracle's closed form."""
