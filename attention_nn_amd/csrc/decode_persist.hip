@@ -327,7 +327,14 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
   }
 }
 
-template <int DH, int BM, int UD>
+// DM, HM: the model dimension and head count as compile-time constants (0:
+// read from P).  The kernel holds more uniform values than the 102 scalar
+// registers of a wave and spills the rest to vector-register lanes, every
+// reload an extra instruction in the phase that needs it; with d and H
+// constant their derived sizes and the divisions by them fold away.  155M
+// batch-1 generation (d 768, H 6): 171 -> 112 spilled scalars, 179.7 ->
+// 168.0 ms (alternating A/B, three rounds, one box).
+template <int DH, int BM, int UD, int DM = 0, int HM = 0>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int KU = DH / 32;       // K slices per lane per chunk (4 lanes per key)
   constexpr int VD = DH / 64;       // output dims per lane in P.V
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = gridDim.x, g = blockIdx.x;
-  const int d = P.d, H = P.H, d2 = d >> 1;
+  const int d = DM ? DM : P.d, H = HM ? HM : P.H, d2 = d >> 1;
   // this work-group's copy of the x' / x exchange (spreads the pollers of
   // each word over rep copies)
   const u64* xm_me = P.xm + (size_t)(g % P.rep) * P.rep_stride;
@@ -422,14 +429,17 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       const int k0 = lo + s * per;
       const int k1 = min(p + 1, k0 + per);
       const int nch = k1 > k0 ? (k1 - k0 + PD_KW - 1) / PD_KW : 0;
-      const int nt = nch > wv ? (nch - wv + PD_NW - 1) / PD_NW : 0;
+      // the wave index as a scalar: its chunk count and key positions are
+      // uniform (scalar branches); part of the measured change above
+      const int wvs = __builtin_amdgcn_readfirstlane(wv);
+      const int nt = nch > wvs ? (nch - wvs + PD_NW - 1) / PD_NW : 0;
       const size_t ho = (((size_t)b * H + h) * P.max_ctx) * DH;
       bf16_t* kcl = P.kc + P.kvl * l;
       bf16_t* vcl = P.vc + P.kvl * l;
       const bf16_t* kh = kcl + ho;
       const bf16_t* vh = vcl + ho;
       const int sk = lane >> 2, sd = (lane & 3) * (DH / 4);   // score: key, first dim
-      auto cbase = [&](int t) { return k0 + PD_KW * (wv + PD_NW * t); };
+      auto cbase = [&](int t) { return k0 + PD_KW * (wvs + PD_NW * t); };
       // K: 4 lanes x Dh/4 dims per key; V: every key's VD dims of this lane
       auto load = [&](int t, uint4* kr, uint32_t* vr) {
         const int c = cbase(t);
@@ -820,9 +830,9 @@ size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
 // step cheaper than a cooperative one (which the runtime serialises), and the
 // bounded waits end the kernel with the error flag set should residency ever
 // fail.  coop: use the cooperative launch instead.
-template <int DH, int BM, int UD>
+template <int DH, int BM, int UD, int DM = 0, int HM = 0>
 static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hipStream_t st) {
-  const void* fn = (const void*)k_decode_persist<DH, BM, UD>;
+  const void* fn = (const void*)k_decode_persist<DH, BM, UD, DM, HM>;
   static bool attr = false;
   if (!attr) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -842,7 +852,12 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hip
 
 template <int BM>
 static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool coop,
-                              hipStream_t st) {
+                              bool spec, hipStream_t st) {
+  // the 155M model's shape (d 768, H 6 x 128) at one row: its own instance
+  if constexpr (BM == 1) {
+    if (spec && Dh == 128 && P.d == 768 && P.H == 6)
+      return pd_launch<128, 1, 2, 768, 6>(P, G, lds, coop, st);
+  }
   switch (Dh * 16 + decode_persist_slots(P.d)) {
     case 64 * 16 + 1: return pd_launch<64, BM, 1>(P, G, lds, coop, st);
     case 64 * 16 + 2: return pd_launch<64, BM, 2>(P, G, lds, coop, st);
@@ -860,7 +875,8 @@ static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool
   return hipErrorInvalidValue;
 }
 
-hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st) {
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, bool specialize,
+                          hipStream_t st) {
   const size_t lds = decode_persist_lds(B, P.d, P.H, Dh, P.s_long);
   if (lds > PD_MAX_LDS || B < 1 || B > PD_MAX_B) return hipErrorInvalidValue;
   // the attention work-groups leave at least one for the o rows, each within
@@ -871,10 +887,10 @@ hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hi
   if (P.head_xcd && !decode_persist_xcd_ok(B, P.d, P.H, Dh, G, P.s_long))
     return hipErrorInvalidValue;
   switch (B) {
-    case 1: return pd_dispatch<1>(P, Dh, G, lds, coop, st);
-    case 2: return pd_dispatch<2>(P, Dh, G, lds, coop, st);
-    case 3: return pd_dispatch<3>(P, Dh, G, lds, coop, st);
-    case 4: return pd_dispatch<4>(P, Dh, G, lds, coop, st);
+    case 1: return pd_dispatch<1>(P, Dh, G, lds, coop, specialize, st);
+    case 2: return pd_dispatch<2>(P, Dh, G, lds, coop, specialize, st);
+    case 3: return pd_dispatch<3>(P, Dh, G, lds, coop, specialize, st);
+    case 4: return pd_dispatch<4>(P, Dh, G, lds, coop, specialize, st);
     default: return hipErrorInvalidValue;
   }
 }

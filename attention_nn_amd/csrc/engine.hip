@@ -234,6 +234,9 @@ struct ann_ctx {
   // one row: each head's qkv rows and attention splits on one XCD where the
   // shapes allow (ANN_PD_XCD=0: contiguous over the work-groups)
   bool pd_xcd_env = true;
+  // the persistent step's compile-time instance for the 155M shape
+  // (ANN_PD_SPECIALIZE=0: the generic kernel)
+  bool pd_spec_env = true;
   // measurement: HIP event pairs around every launch of one kernel class
   int prof_kind = -1;
   std::vector<hipEvent_t> prof_ev;
@@ -706,7 +709,7 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.eps = g.rms_eps;
   {
     ProfScope ps(c, ANN_PROF_STEP, st);
-    HIPCHK(decode_persist(P, B, c->Dh, c->pd_g, c->pd_coop, st));
+    HIPCHK(decode_persist(P, B, c->Dh, c->pd_g, c->pd_coop, c->pd_spec_env, st));
   }
   if (cands) {
     int holders = 0;   // work-groups whose rows start below Vs
@@ -783,6 +786,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->pd_on = on && atoi(on) > 0 ? atoi(on) : 0;
   const char* px = getenv("ANN_PD_XCD");
   c->pd_xcd_env = !(px && px[0] == '0');
+  const char* ps = getenv("ANN_PD_SPECIALIZE");
+  c->pd_spec_env = !(ps && ps[0] == '0');
   const char* pr = getenv("ANN_PD_REP");
   if (pr && atoi(pr) >= 1 && atoi(pr) <= PD_MAX_REP) c->pd_rep = atoi(pr);
   const char* ds = getenv("ANN_DEC_SPLITS");

@@ -290,7 +290,10 @@ constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffer
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 bool decode_persist_xcd_ok(int B, int d, int H, int Dh, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
-hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, hipStream_t st);
+// specialize: take the compile-time instance of a model shape that has one
+// (155M at one row), else the generic kernel
+hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, bool specialize,
+                          hipStream_t st);
 
 hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st);
 hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,

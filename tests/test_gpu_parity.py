@@ -756,23 +756,26 @@ def test_persistent_155m_late_positions_match_oracle():
     assert worst < LOGIT_TOL, worst
 
 
-def test_persistent_155m_head_xcd_layout_bitwise(monkeypatch):
-    """The persistent step's two work layouts at 155M: each head's qkv rows and
-    attention splits on XCD h (the default where the shares divide: 192
-    work-groups, 8 row pairs each) against the rows split contiguously over
-    all work-groups (ANN_PD_XCD=0).  Every row and every attention unit is
-    computed the same way in both, so the logits of a 500-token prefill's
-    decode steps (windowed layers over three splits, full-causal over eight)
-    are bitwise equal, greedy and teacher-forced."""
+@pytest.mark.parametrize("var", ["ANN_PD_XCD", "ANN_PD_SPECIALIZE"])
+def test_persistent_155m_variants_bitwise(var, monkeypatch):
+    """The persistent step at 155M against two of its variants, teacher-forced
+    decode steps after a 500-token prefill (windowed layers over three splits,
+    full-causal over eight), logits bitwise equal:
+    ANN_PD_XCD=0 splits the qkv rows contiguously over all work-groups
+    instead of each head's rows and attention splits on XCD h (the default
+    where the shares divide: 192 work-groups, 8 row pairs each);
+    ANN_PD_SPECIALIZE=0 runs the generic kernel instead of the instance with
+    the 155M model's d and H as compile-time constants.  Every row and
+    attention unit is computed the same way in each pair."""
     cfg = cfg_155m()
     p = perturb_lambdas(init_params(cfg, 13, dense=True))
     tok = np.random.default_rng(131).integers(0, 50257, (1, 520))
 
-    def run(xcd):
-        monkeypatch.setenv("ANN_PD_XCD", xcd)
+    def run(val):
+        monkeypatch.setenv(var, val)
         eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
-        monkeypatch.delenv("ANN_PD_XCD")
-        print(f"case 155M batch 1, ANN_PD_XCD={xcd}: prefill 500, 20 decode steps", flush=True)
+        monkeypatch.delenv(var)
+        print(f"case 155M batch 1, {var}={val}: prefill 500, 20 decode steps", flush=True)
         eng.prefill(tok[:, :500])
         lgs = []
         for i in range(500, 520):
