@@ -333,8 +333,10 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
 // reload an extra instruction in the phase that needs it; with d and H
 // constant their derived sizes and the divisions by them fold away.  155M
 // batch-1 generation (d 768, H 6): 171 -> 112 spilled scalars, 179.7 ->
-// 168.0 ms (alternating A/B, three rounds, one box).
-template <int DH, int BM, int UD, int DM = 0, int HM = 0>
+// 168.0 ms (alternating A/B, three rounds, one box).  GR: greedy without
+// fp32 logits at compile time (no z, candidate or logits stores; 170.8 ->
+// 169.6 ms on the same shape).
+template <int DH, int BM, int UD, int DM = 0, int HM = 0, int GR = 0>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int KU = DH / 32;       // K slices per lane per chunk (4 lanes per key)
   constexpr int VD = DH / 64;       // output dims per lane in P.V
@@ -356,6 +358,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = gridDim.x, g = blockIdx.x;
   const int d = DM ? DM : P.d, H = HM ? HM : P.H, d2 = d >> 1;
+  const bool greedy = GR ? true : (P.greedy != 0);
+  float* const logits = GR ? nullptr : P.logits;
+  uint32_t* const cand = GR ? nullptr : P.cand;
   // this work-group's copy of the x' / x exchange (spreads the pollers of
   // each word over rep copies)
   const u64* xm_me = P.xm + (size_t)(g % P.rep) * P.rep_stride;
@@ -677,14 +682,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         for (int b = 0; b < BM; ++b) {
           const float y = wave_sum(acc[b]);
           const bf16_t zb = f2bf(y);
-          if (P.greedy) {
+          if (greedy) {
             const u64 key = n < P.Vs ? (((u64)zkey(zb) << 16) | (u64)(0xffffu - (uint32_t)n)) : 0ull;
             best[b] = key > best[b] ? key : best[b];
           } else if (lane == 0) {
             P.z[(size_t)b * P.V + n] = zb;
-            if (P.cand) zsl[b * nrow + r] = zb;
+            if (cand) zsl[b * nrow + r] = zb;
           }
-          if (P.logits && lane == 0) P.logits[(size_t)b * P.V + n] = softcap(bf2f(zb));
+          if (logits && lane == 0) logits[(size_t)b * P.V + n] = softcap(bf2f(zb));
         }
       }
     }
@@ -704,7 +709,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     hdot(k + 1, wb);
   }
 
-  if (!P.greedy && P.cand) {
+  if (!greedy && cand) {
     // candidates of this work-group's slice (sample_cand): wave b < BM takes
     // row b, lane l the entries l + 64 i; TK_M + 1 rounds of a wave maximum
     // over the lanes' largest words, each popped from its lane
@@ -729,11 +734,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
 #pragma unroll
         for (int i = 0; i < PD_ZE; ++i) w[i] = w[i] == gm ? 0u : w[i];
       }
-      if (lane < TK_M) P.cand[((size_t)b * G + g) * TK_M + lane] = mine;
+      if (lane < TK_M) cand[((size_t)b * G + g) * TK_M + lane] = mine;
       else if (lane == TK_M) P.cand_r[(size_t)b * G + g] = mine;
     }
   }
-  if (P.greedy) {
+  if (greedy) {
     if (lane == 0) {
 #pragma unroll
       for (int b = 0; b < BM; ++b) s_key[b][wv] = best[b];
@@ -830,9 +835,9 @@ size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long) {
 // step cheaper than a cooperative one (which the runtime serialises), and the
 // bounded waits end the kernel with the error flag set should residency ever
 // fail.  coop: use the cooperative launch instead.
-template <int DH, int BM, int UD, int DM = 0, int HM = 0>
+template <int DH, int BM, int UD, int DM = 0, int HM = 0, int GR = 0>
 static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hipStream_t st) {
-  const void* fn = (const void*)k_decode_persist<DH, BM, UD, DM, HM>;
+  const void* fn = (const void*)k_decode_persist<DH, BM, UD, DM, HM, GR>;
   static bool attr = false;
   if (!attr) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -853,10 +858,12 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hip
 template <int BM>
 static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool coop,
                               bool spec, hipStream_t st) {
-  // the 155M model's shape (d 768, H 6 x 128) at one row: its own instance
+  // the 155M model's shape (d 768, H 6 x 128) at one row: its own instances
   if constexpr (BM == 1) {
-    if (spec && Dh == 128 && P.d == 768 && P.H == 6)
+    if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
+      if (P.greedy && !P.logits) return pd_launch<128, 1, 2, 768, 6, 1>(P, G, lds, coop, st);
       return pd_launch<128, 1, 2, 768, 6>(P, G, lds, coop, st);
+    }
   }
   switch (Dh * 16 + decode_persist_slots(P.d)) {
     case 64 * 16 + 1: return pd_launch<64, BM, 1>(P, G, lds, coop, st);
