@@ -363,8 +363,21 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   uint32_t* const cand = GR ? nullptr : P.cand;
   // this work-group's copy of the x' / x exchange (spreads the pollers of
   // each word over rep copies)
-  const u64* xm_me = P.xm + (size_t)(g % P.rep) * P.rep_stride;
-  const u64* xx_me = P.xx + (size_t)(g % P.rep) * P.rep_stride;
+  // exchange areas: with d and H constant, their offsets from xq and the
+  // copy strides are compile-time constants (fewer live scalars)
+  u64* const xq = P.xq;
+  u64* const xp = DM ? xq + pd_layout(DM, HM ? HM : 1, 2) / 8 : P.xp;
+  u64* const xm = DM ? xq + pd_layout(DM, HM ? HM : 1, 3) / 8 : P.xm;
+  u64* const xh = DM ? xq + pd_layout(DM, HM ? HM : 1, 4) / 8 : P.xh;
+  u64* const xx = DM ? xq + pd_layout(DM, HM ? HM : 1, 5) / 8 : P.xx;
+  u64* const xk = DM ? xq + pd_layout(DM, HM ? HM : 1, 6) / 8 : P.xk;
+  unsigned* const gen = DM ? (unsigned*)(xq + pd_layout(DM, HM ? HM : 1, 7) / 8) : P.gen;
+  unsigned* const err = DM ? (unsigned*)(xq + pd_layout(DM, HM ? HM : 1, 8) / 8) : P.err;
+  const int rep_stride = DM ? (int)pd_rep_stride(DM) : P.rep_stride;
+  const int h_stride = DM ? (int)pd_h_stride(DM) : P.h_stride;
+  const int p_stride = DM ? (int)pd_p_stride(DM, HM ? HM : 1) : P.p_stride;
+  const u64* xm_me = xm + (size_t)(g % P.rep) * rep_stride;
+  const u64* xx_me = xx + (size_t)(g % P.rep) * rep_stride;
   bf16_t* sx0 = (bf16_t*)lds4;        // x0 (BM x d)
   bf16_t* sxs = sx0 + BM * d;         // layer input x
   bf16_t* sxm = sxs + BM * d;         // x after attention
@@ -373,7 +386,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
                                       // waves poll it while others may still read gin
   float* spart = (float*)(ghb + BM * 4 * d);   // attention partials
 
-  const uint32_t tb = __hip_atomic_load(P.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * PD_PH;
+  const uint32_t tb = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * PD_PH;
   if (tid < BM) s_pos[tid] = P.pos[tid];
 
   // layer 0's qkv weights first: their loads do not depend on the token
@@ -407,11 +420,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     pd_rows_qkv<P2>(P.head_xcd, H, d2, n0, nr);
     if (l > 0) pd_wload2<UD>(Wl + P.o_qkv, d, n0, nr, wr);
     if (l > 0) {
-      ll_poll(xx_me, BM * d2, (uint32_t*)sxs, t1 - 1u, P.err);
+      ll_poll(xx_me, BM * d2, (uint32_t*)sxs, t1 - 1u, err);
       __syncthreads();
     }
     pd_rms<BM>(sxs, gin, d, P.eps, red);
-    pd_wdot2<PE_STORE, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xq, 3 * d2, t1, lam, nullptr,
+    pd_wdot2<PE_STORE, UD, BM>(wr, (const uint4*)gin, d, n0, nr, xq, 3 * d2, t1, lam, nullptr,
                                nullptr, d, 1, 0);
 
     // ---- 2: attention of (b, h, split)
@@ -475,10 +488,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         rsn = P.sn[(size_t)p * D4 + tid];
       }
       // q, k, v of this head from phase 1
-      const u64* src = P.xq + (size_t)b * 3 * d2 + h * P2;
+      const u64* src = xq + (size_t)b * 3 * d2 + h * P2;
       for (int i = tid; i < 3 * P2; i += PD_T) {
         const int part = i / P2, k = i - part * P2;
-        s_in[i] = ll_wait(src + part * d2 + k, t1, P.err);
+        s_in[i] = ll_wait(src + part * d2 + k, t1, err);
       }
       __syncthreads();
       if (tid < 64) {   // QK-norm + RoPE, one dim pair per lane (lanes >= Dh/2 idle)
@@ -570,20 +583,20 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       for (int e = 0; e < VD; ++e) s_o[wv][VD * lane + e] = acc[e];
       if (lane == 0) s_l[wv] = lsum;
       __syncthreads();
-      u64* dst = P.xp + (size_t)au * (DH + 1);
+      u64* dst = xp + (size_t)au * (DH + 1);
       if (tid < DH) {
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < PD_NW; ++w) o += s_o[w][tid];
         for (int c = 0; c < PD_REP_P; ++c)
-          ll_store(dst + (size_t)c * P.p_stride + tid, __float_as_uint(o), t1 + 1u);
+          ll_store(dst + (size_t)c * p_stride + tid, __float_as_uint(o), t1 + 1u);
       }
       if (tid == 0) {
         float lt = 0.f;
 #pragma unroll
         for (int w = 0; w < PD_NW; ++w) lt += s_l[w];
         for (int c = 0; c < PD_REP_P; ++c)
-          ll_store(dst + (size_t)c * P.p_stride + DH, __float_as_uint(lt), t1 + 1u);
+          ll_store(dst + (size_t)c * p_stride + DH, __float_as_uint(lt), t1 + 1u);
       }
     }
 
@@ -596,7 +609,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
     // the exchange.
     if (!attn) {
       const int nw = BM * H * S * (DH + 1);
-      ll_poll(P.xp + (size_t)(g % PD_REP_P) * P.p_stride, nw, (uint32_t*)spart, t1 + 1u, P.err);
+      ll_poll(xp + (size_t)(g % PD_REP_P) * p_stride, nw, (uint32_t*)spart, t1 + 1u, err);
       __syncthreads();
       for (int i = tid; i < BM * d; i += PD_T) {
         const int b = i / d, c = i - b * d, h = c / DH, e = c - h * DH;
@@ -609,26 +622,26 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         gin[i] = f2bf(o / lt);
       }
       __syncthreads();
-      pd_wdot2<PE_ATTN, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xm, d2, t1 + 2u, lam, sxs, sx0, d,
-                                P.rep, P.rep_stride);
+      pd_wdot2<PE_ATTN, UD, BM>(wr, (const uint4*)gin, d, n0, nr, xm, d2, t1 + 2u, lam, sxs, sx0, d,
+                                P.rep, rep_stride);
     }
 
     // ---- 4: h = relu2(rms(x') Wfc^T)
     pd_rows(2 * d, n0, nr, 0, G);
     pd_wload2<UD>(Wl + P.o_fc, d, n0, nr, wr);
-    ll_poll(xm_me, BM * d2, (uint32_t*)sxm, t1 + 2u, P.err);
+    ll_poll(xm_me, BM * d2, (uint32_t*)sxm, t1 + 2u, err);
     __syncthreads();
     pd_rms<BM>(sxm, gin, d, P.eps, red);
-    pd_wdot2<PE_RELU2, UD, BM>(wr, (const uint4*)gin, d, n0, nr, P.xh, 2 * d, t1 + 3u, lam, nullptr,
-                               nullptr, d, PD_REP_H, P.h_stride);
+    pd_wdot2<PE_RELU2, UD, BM>(wr, (const uint4*)gin, d, n0, nr, xh, 2 * d, t1 + 3u, lam, nullptr,
+                               nullptr, d, PD_REP_H, h_stride);
 
     // ---- 5: x = mix_mlp(x', h Wproj^T)
     pd_rows(d2, n0, nr, 0, G);
     pd_wload<4 * UD, 1>(Wl + P.o_proj, 4 * d, n0, nr, wr);
-    ll_poll(P.xh + (size_t)(g % PD_REP_H) * P.h_stride, BM * 2 * d, (uint32_t*)ghb, t1 + 3u, P.err);
+    ll_poll(xh + (size_t)(g % PD_REP_H) * h_stride, BM * 2 * d, (uint32_t*)ghb, t1 + 3u, err);
     __syncthreads();
     pd_wdot<4 * UD, 1, BM>(wr, (const uint4*)ghb, 4 * d, nr, stage);
-    pd_emit<PE_MLP, BM>(stage, n0, nr, P.xx, d2, t1 + 4u, lam, sxm, nullptr, d, P.rep, P.rep_stride);
+    pd_emit<PE_MLP, BM>(stage, n0, nr, xx, d2, t1 + 4u, lam, sxm, nullptr, d, P.rep, rep_stride);
   }
 
   // ---- lm_head over this work-group's rows [r0, r1), two register batches
@@ -699,7 +712,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   uint4 wa[PD_HS], wb[PD_HS];
   const int nbe = (nb + 1) & ~1;
   if (nb > 0) hload(0, wa);
-  ll_poll(xx_me, BM * d2, (uint32_t*)sxs, tl, P.err);
+  ll_poll(xx_me, BM * d2, (uint32_t*)sxs, tl, err);
   __syncthreads();
   pd_rms<BM>(sxs, gin, d, P.eps, red);
   for (int k = 0; k < nbe; k += 2) {
@@ -748,7 +761,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       u64 m = 0;
 #pragma unroll
       for (int w = 0; w < PD_NW; ++w) m = s_key[tid][w] > m ? s_key[tid][w] : m;
-      ll_store(P.xk + (size_t)g * BM + tid, (uint32_t)m, tl + 1u);
+      ll_store(xk + (size_t)g * BM + tid, (uint32_t)m, tl + 1u);
     }
     if (g == 0) {   // token = largest key over all work-groups
       u64 m[BM];
@@ -757,7 +770,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       for (int i = tid; i < G; i += PD_T) {
 #pragma unroll
         for (int b = 0; b < BM; ++b) {
-          const u64 v = ll_wait(P.xk + (size_t)i * BM + b, tl + 1u, P.err);
+          const u64 v = ll_wait(xk + (size_t)i * BM + b, tl + 1u, err);
           m[b] = v > m[b] ? v : m[b];
         }
       }
@@ -785,7 +798,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   // every work-group read the generation before its first output and work-
   // group 0 has consumed outputs of all of them: advance it for the next step
   if (g == 0 && tid == 0)
-    __hip_atomic_store(P.gen, (tb / PD_PH) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gen, (tb / PD_PH) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -855,12 +868,26 @@ static hipError_t pd_launch(const PDParams& P, int G, size_t lds, bool coop, hip
   return hipLaunchKernel(fn, dim3(G), dim3(PD_T), args, lds, st);
 }
 
+// Whether P's exchange areas and strides are the ones pd_layout places from
+// P.xq (what a compile-time-shape instance assumes).
+static bool pd_areas_match(const PDParams& P) {
+  const size_t d = (size_t)P.d, H = (size_t)P.H;
+  const char* q = (const char*)P.xq;
+  const void* areas[7] = {P.xp, P.xm, P.xh, P.xx, P.xk, P.gen, P.err};
+  for (int i = 0; i < 7; ++i)
+    if ((const char*)areas[i] != q + pd_layout(d, H, i + 2)) return false;
+  return (size_t)P.rep_stride == pd_rep_stride(d) && (size_t)P.h_stride == pd_h_stride(d) &&
+         (size_t)P.p_stride == pd_p_stride(d, H);
+}
+
 template <int BM>
 static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool coop,
                               bool spec, hipStream_t st) {
   // the 155M model's shape (d 768, H 6 x 128) at one row: its own instances
+  // (which derive the exchange areas from xq: the caller's must match)
   if constexpr (BM == 1) {
     if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
+      if (!pd_areas_match(P)) return hipErrorInvalidValue;
       if (P.greedy && !P.logits) return pd_launch<128, 1, 2, 768, 6, 1>(P, G, lds, coop, st);
       return pd_launch<128, 1, 2, 768, 6>(P, G, lds, coop, st);
     }

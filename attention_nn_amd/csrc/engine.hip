@@ -79,30 +79,8 @@ struct SLayout {  // byte offsets into the workspace
       ce, ce_tz, ce_rows, ce_mean, total;
 };
 
-// Exchange area of the persistent decode step (up to PD_MAX_B rows): tagged
-// words of xq, xp, xm, xh, xx, xk, then the generation and error words.  xm
-// and xx hold PD_MAX_REP copies pd_rep_stride words apart; xp and xh have
-// room for PD_MAX_REP copies pd_p_stride / pd_h_stride apart, of which the
-// step uses PD_REP_P / PD_REP_H (the measured layout: packing the areas
-// tighter moved the step's time by up to 2.7%).  With `which` = 1..8 returns
-// the byte offset of that part, 0 the total size.
-constexpr int PD_MAX_SLONG = 8;
-constexpr int PD_MAX_G = 1024;
-size_t pd_rep_stride(const ann_config& c) { return ((size_t)PD_MAX_B * c.d / 2 + 63) / 64 * 64; }
-size_t pd_h_stride(const ann_config& c) { return ((size_t)PD_MAX_B * 2 * c.d + 63) / 64 * 64; }
-size_t pd_p_stride(const ann_config& c) {
-  return ((size_t)PD_MAX_B * c.H * PD_MAX_SLONG * (c.d / c.H + 1) + 63) / 64 * 64;
-}
 size_t pd_layout(const ann_config& c, int which) {
-  const size_t d = c.d, B = PD_MAX_B, rs = pd_rep_stride(c);
-  const size_t parts[8] = {B * 3 * d / 2, PD_MAX_REP * pd_p_stride(c), PD_MAX_REP * rs,
-                           PD_MAX_REP * pd_h_stride(c), PD_MAX_REP * rs, (size_t)PD_MAX_G * B, 1, 1};
-  size_t off = 0;
-  for (int i = 0; i < 8; ++i) {
-    if (which == i + 1) return off;
-    off += up(parts[i] * 8);
-  }
-  return off;
+  return ann::pd_layout((size_t)c.d, (size_t)c.H, which);
 }
 
 // 128-column tiles of the lm_head GEMM (its work-group tile width).
@@ -700,9 +678,9 @@ int enqueue_persist(ann_ctx* c, const int32_t* tokens, int B, bool greedy, int32
   P.greedy = greedy ? 1 : 0;
   P.rep = c->pd_rep;
   P.on = c->pd_on > 0 ? c->pd_on : g.d / 8;
-  P.rep_stride = (int)pd_rep_stride(g);
-  P.h_stride = (int)pd_h_stride(g);
-  P.p_stride = (int)pd_p_stride(g);
+  P.rep_stride = (int)pd_rep_stride(g.d);
+  P.h_stride = (int)pd_h_stride(g.d);
+  P.p_stride = (int)pd_p_stride(g.d, g.H);
   P.head_xcd = c->pd_xcd_env && decode_persist_xcd_ok(B, g.d, g.H, c->Dh, G, P.s_long) ? 1 : 0;
   P.scale = g.attn_scale;
   P.shift = g.attn_scale * (float)c->Dh * 1.02f;

@@ -287,6 +287,38 @@ constexpr int PD_MAX_B = 4;                       // rows of the persistent step
 // work-group's vocabulary slice of at most 64 PD_ZE rows
 constexpr int PD_ZE = 8;
 constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffers + partials)
+constexpr int PD_MAX_SLONG = 8;                   // attention splits per (row, head)
+constexpr int PD_MAX_G = 1024;                    // work-groups
+
+// Exchange area of the persistent decode step (up to PD_MAX_B rows), in
+// 64-bit words: tagged words of xq, xp, xm, xh, xx, xk, then the generation
+// and error words.  xm and xx hold PD_MAX_REP copies pd_rep_stride words
+// apart; xp and xh have room for PD_MAX_REP copies pd_p_stride / pd_h_stride
+// apart, of which the step uses PD_REP_P / PD_REP_H (the measured layout:
+// packing the areas tighter moved the step's time by up to 2.7%).  Functions
+// of d and H only, so a kernel instance with both as constants derives every
+// area from xq at compile time.
+constexpr size_t pd_round64(size_t v) { return (v + 63) / 64 * 64; }
+constexpr size_t pd_rep_stride(size_t d) { return pd_round64((size_t)PD_MAX_B * d / 2); }
+constexpr size_t pd_h_stride(size_t d) { return pd_round64((size_t)PD_MAX_B * 2 * d); }
+constexpr size_t pd_p_stride(size_t d, size_t H) {
+  return pd_round64((size_t)PD_MAX_B * H * PD_MAX_SLONG * (d / H + 1));
+}
+// Byte offset of part `which` (1..8) from the area's start (256-byte aligned
+// parts), 0: the total size.
+constexpr size_t pd_layout(size_t d, size_t H, int which) {
+  const size_t B = PD_MAX_B, rs = pd_rep_stride(d);
+  const size_t parts[8] = {B * 3 * d / 2,        PD_MAX_REP * pd_p_stride(d, H),
+                           PD_MAX_REP * rs,        PD_MAX_REP * pd_h_stride(d),
+                           PD_MAX_REP * rs,        (size_t)PD_MAX_G * B,
+                           1,                      1};
+  size_t off = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (which == i + 1) return off;
+    off += (parts[i] * 8 + 255) / 256 * 256;
+  }
+  return off;
+}
 bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s_long);
 bool decode_persist_xcd_ok(int B, int d, int H, int Dh, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
