@@ -474,8 +474,9 @@ def main():
                      "traffic": step_traffic(),
                      "traffic_source": "profiles/decode_persist_b1_hbm_traffic.md (rocprofv3 "
                                        "FETCH_SIZE/WRITE_SIZE)",
-                     "kernel": "k_decode_persist<128,1,2> (whole batch-1 decode step: embed, 11 "
-                               "layers, lm_head + softcap, greedy argmax)",
+                     "kernel": "k_decode_persist<128,1,2,768,6,1> (the 155M greedy instance of the "
+                               "whole batch-1 decode step: embed, 11 layers, lm_head + softcap, "
+                               "greedy argmax)",
                      "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(k_avg_ms * 1e3, 3),
                      "avg_launch_source": "median decode segment of the timed generations / "
                                           f"{n_decode} back-to-back launches",
