@@ -766,26 +766,27 @@ def test_persistent_155m_late_positions_match_oracle():
     assert worst < LOGIT_TOL, worst
 
 
-@pytest.mark.parametrize("var", ["ANN_PD_XCD", "ANN_PD_SPECIALIZE"])
-def test_persistent_155m_variants_bitwise(var, monkeypatch):
+@pytest.mark.parametrize("var,B", [("ANN_PD_XCD", 1), ("ANN_PD_SPECIALIZE", 1),
+                                   ("ANN_PD_SPECIALIZE", 2)])
+def test_persistent_155m_variants_bitwise(var, B, monkeypatch):
     """The persistent step at 155M against two of its variants, teacher-forced
     decode steps after a 500-token prefill (windowed layers over three splits,
-    full-causal over eight), logits bitwise equal:
+    full-causal over eight at one row), logits bitwise equal:
     ANN_PD_XCD=0 splits the qkv rows contiguously over all work-groups
     instead of each head's rows and attention splits on XCD h (the default
     where the shares divide: 192 work-groups, 8 row pairs each);
     ANN_PD_SPECIALIZE=0 runs the generic kernel instead of the instance with
-    the 155M model's d and H as compile-time constants.  Every row and
-    attention unit is computed the same way in each pair."""
+    the 155M model's d and H as compile-time constants (one and two rows).
+    Every row and attention unit is computed the same way in each pair."""
     cfg = cfg_155m()
     p = perturb_lambdas(init_params(cfg, 13, dense=True))
-    tok = np.random.default_rng(131).integers(0, 50257, (1, 520))
+    tok = np.random.default_rng(131).integers(0, 50257, (B, 520))
 
     def run(val):
         monkeypatch.setenv(var, val)
-        eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+        eng = _engine(cfg, p, B, ctx=1024, tokens=B * 512)
         monkeypatch.delenv(var)
-        print(f"case 155M batch 1, {var}={val}: prefill 500, 20 decode steps", flush=True)
+        print(f"case 155M {B} rows, {var}={val}: prefill 500, 20 decode steps", flush=True)
         eng.prefill(tok[:, :500])
         lgs = []
         for i in range(500, 520):
