@@ -108,7 +108,7 @@ __device__ __forceinline__ void pd_rows(int npairs, int& n0, int& nr, int first,
 }
 
 // qkv rows of work-group g.  With xcd (one row, H <= 8, shares checked by
-// decode_persist_xq_ok) the q, k and v rows of head h come from the
+// decode_persist_xcd_ok) the q, k and v rows of head h come from the
 // work-groups of XCD h (work-group g runs on XCD g % 8), which also run that
 // head's attention splits, so that hand-off stays inside one XCD: the 3 Dh/2
 // row pairs of the head split evenly over the XCD's G / 8 work-groups, each
@@ -361,8 +361,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   const bool greedy = GR ? true : (P.greedy != 0);
   float* const logits = GR ? nullptr : P.logits;
   uint32_t* const cand = GR ? nullptr : P.cand;
-  // this work-group's copy of the x' / x exchange (spreads the pollers of
-  // each word over rep copies)
   // exchange areas: with d and H constant, their offsets from xq and the
   // copy strides are compile-time constants (fewer live scalars)
   u64* const xq = P.xq;
@@ -376,6 +374,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   const int rep_stride = DM ? (int)pd_rep_stride(DM) : P.rep_stride;
   const int h_stride = DM ? (int)pd_h_stride(DM) : P.h_stride;
   const int p_stride = DM ? (int)pd_p_stride(DM, HM ? HM : 1) : P.p_stride;
+  // this work-group's copy of the x' / x exchange (spreads the pollers of
+  // each word over rep copies)
   const u64* xm_me = xm + (size_t)(g % P.rep) * rep_stride;
   const u64* xx_me = xx + (size_t)(g % P.rep) * rep_stride;
   bf16_t* sx0 = (bf16_t*)lds4;        // x0 (BM x d)
