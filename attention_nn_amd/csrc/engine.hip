@@ -201,12 +201,14 @@ struct ann_ctx {
   // decode attention: splits per (row, head) fixed by ANN_DEC_SPLITS (0: sized
   // by the batch, about 384 work-groups)
   int dec_split_env = 0;
-  // rows the persistent step takes by default: its GEMV-style phases apply
-  // every weight to each row in turn, so a row costs ~60 us more (155M
-  // decode step at 1 / 2 / 3 / 4 rows: 185 / 256 / 308 / 370 us against
-  // 258 / 301 / 320 / 326 us on the per-kernel path, measured);
-  // ANN_PERSIST_MAX_B (1..PD_MAX_B) changes it
-  int pd_max_b = 3;
+  // rows the persistent step takes by default (0: by shape): its GEMV-style
+  // phases apply every weight to each row in turn, so a row costs 40-60 us
+  // more.  155M decode step at 1 / 2 / 3 / 4 rows, generic kernel: 185 / 256
+  // / 308 / 370 us, against 258 / 301 / 320 / 326 us on the per-kernel path;
+  // with the 155M instances 4 rows take 314 against 325 us (sampled 323
+  // against 331), so that shape takes up to 4 rows, any other up to 3.
+  // ANN_PERSIST_MAX_B (1..PD_MAX_B) fixes it
+  int pd_max_b = 0;
   int pd_rep = PD_MAX_REP;   // copies of the persistent step's x' / x exchange
   int pd_on = 0;             // work-groups for the o rows (0: d / 8, 8 rows each)
   // one row: each head's qkv rows and attention splits on one XCD where the
@@ -583,7 +585,9 @@ int pd_splits(const ann_ctx* c, int B, bool lng) {
 
 // Whether this decode step runs as the persistent kernel.
 bool persist_ok(ann_ctx* c, int B) {
-  if (!c->pd_env || B < 1 || B > c->pd_max_b ||
+  const int max_b = c->pd_max_b > 0 ? c->pd_max_b
+                    : (c->pd_spec_env && c->c.d == 768 && c->c.H == 6 && c->Dh == 128) ? 4 : 3;
+  if (!c->pd_env || B < 1 || B > max_b ||
       (c->prof_kind >= 0 && c->prof_kind != ANN_PROF_STEP))
     return false;
   const ann_config& g = c->c;

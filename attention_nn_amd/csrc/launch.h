@@ -323,7 +323,7 @@ bool decode_persist_fits(int B, int d, int H, int Dh, int V, int L, int G, int s
 bool decode_persist_xcd_ok(int B, int d, int H, int Dh, int G, int s_long);
 size_t decode_persist_lds(int B, int d, int H, int Dh, int s_long);
 // specialize: take the compile-time instance of a model shape that has one
-// (155M at 1-3 rows), else the generic kernel
+// (155M at 1-4 rows), else the generic kernel
 hipError_t decode_persist(const PDParams& P, int B, int Dh, int G, bool coop, bool specialize,
                           hipStream_t st);
 
