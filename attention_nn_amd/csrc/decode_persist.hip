@@ -551,6 +551,18 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         }
         sc = quad_sum(sc);
         const float pj = j < k1 ? __builtin_amdgcn_exp2f(sc * sl2 - sh2) : 0.f;
+        // a chunk without the new token (all but at most one per step) skips
+        // the per-key test for it: 165.8 -> 164.4 ms per 155M generation
+        if (p < c || p >= c + PD_KW) {
+#pragma unroll
+          for (int u = 0; u < PD_KW; ++u) {
+            const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * u));
+            lsum += pu;
+            acc[0] += pu * __uint_as_float(vr[u] << 16);
+            if (VD == 2) acc[VD - 1] += pu * __uint_as_float(vr[u] & 0xffff0000u);
+          }
+          return;
+        }
 #pragma unroll
         for (int u = 0; u < PD_KW; ++u) {
           const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * u));
