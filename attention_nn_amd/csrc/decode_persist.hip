@@ -536,6 +536,29 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
       auto compute = [&](int t, const uint4* kr, const uint32_t* vr) {
         const int c = cbase(t);
         const int j = c + sk;
+        // a chunk without the new token (all but at most one per step) takes a
+        // score and P.V path without the per-lane / per-key tests for it:
+        // 165.8 -> 161.9 ms per 155M generation (two A/B steps)
+        if (p < c || p >= c + PD_KW) {
+          float sf = 0.f;
+#pragma unroll
+          for (int u = 0; u < KU; ++u) {
+            sf = pd_dot2(qp[4 * u + 0], kr[u].x, sf);
+            sf = pd_dot2(qp[4 * u + 1], kr[u].y, sf);
+            sf = pd_dot2(qp[4 * u + 2], kr[u].z, sf);
+            sf = pd_dot2(qp[4 * u + 3], kr[u].w, sf);
+          }
+          sf = quad_sum(sf);
+          const float pf = j < k1 ? __builtin_amdgcn_exp2f(sf * sl2 - sh2) : 0.f;
+#pragma unroll
+          for (int u = 0; u < PD_KW; ++u) {
+            const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pf), 4 * u));
+            lsum += pu;
+            acc[0] += pu * __uint_as_float(vr[u] << 16);
+            if (VD == 2) acc[VD - 1] += pu * __uint_as_float(vr[u] & 0xffff0000u);
+          }
+          return;
+        }
         float sc = 0.f;
         if (j == p) {
 #pragma unroll
@@ -551,18 +574,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
         }
         sc = quad_sum(sc);
         const float pj = j < k1 ? __builtin_amdgcn_exp2f(sc * sl2 - sh2) : 0.f;
-        // a chunk without the new token (all but at most one per step) skips
-        // the per-key test for it: 165.8 -> 164.4 ms per 155M generation
-        if (p < c || p >= c + PD_KW) {
-#pragma unroll
-          for (int u = 0; u < PD_KW; ++u) {
-            const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * u));
-            lsum += pu;
-            acc[0] += pu * __uint_as_float(vr[u] << 16);
-            if (VD == 2) acc[VD - 1] += pu * __uint_as_float(vr[u] & 0xffff0000u);
-          }
-          return;
-        }
 #pragma unroll
         for (int u = 0; u < PD_KW; ++u) {
           const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * u));
