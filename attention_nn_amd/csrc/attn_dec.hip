@@ -114,7 +114,8 @@ void k_attn_dec(
   __shared__ float s_l[AD_THREADS / 64];
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // the wave index as a scalar (the per-chunk test below is uniform)
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // the ticket is taken first; its value is read after the barriers below
   __shared__ unsigned s_ticket;
   if (nsplit > 1 && tid == 0)
@@ -200,6 +201,32 @@ void k_attn_dec(
   auto compute = [&](int t, const uint4* kr, const uint4* vr4) {
     const int c = chunk_base(t);
     const int j = c + sk;
+    // a chunk without the new token (all but at most one per (row, head))
+    // takes the score and P.V path without the per-lane tests for it:
+    // batch-64 step 0.5498 -> 0.5467 ms, cfg4 0.5026 -> 0.5004 ms
+    if (p < c || p >= c + AD_KW) {
+      float sf = 0.f;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        sf = dot2_bf16(qp[4 * u + 0], kr[u].x, sf);
+        sf = dot2_bf16(qp[4 * u + 1], kr[u].y, sf);
+        sf = dot2_bf16(qp[4 * u + 2], kr[u].z, sf);
+        sf = dot2_bf16(qp[4 * u + 3], kr[u].w, sf);
+      }
+      sf += __shfl_xor(sf, 1, 64);
+      sf += __shfl_xor(sf, 2, 64);
+      const float pf = j < k1 ? __builtin_amdgcn_exp2f(sf * sl2 - sh2) : 0.f;
+      if ((lane & 3) == 0) lsum += pf;
+#pragma unroll
+      for (int u = 0; u < VU; ++u) {
+        const float pr = __shfl(pf, 4 * (vr + u * VP), 64);
+        float vf[8];
+        unpack8(vr4[u], vf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += pr * vf[e];
+      }
+      return;
+    }
     float s = 0.f;
     if (j == p) {
 #pragma unroll
