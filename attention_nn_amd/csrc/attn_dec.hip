@@ -203,8 +203,9 @@ void k_attn_dec(
     const int j = c + sk;
     // a chunk without the new token (all but at most one per (row, head))
     // takes the score and P.V path without the per-lane tests for it:
-    // batch-64 step 0.5498 -> 0.5467 ms, cfg4 0.5026 -> 0.5004 ms
-    if (p < c || p >= c + AD_KW) {
+    // batch-64 step 0.5498 -> 0.5467 ms, cfg4 0.5026 -> 0.5004 ms.  Not in
+    // the register-capped two-chunk ring (cfg5 step 3.055 -> 3.122 ms with it)
+    if (RING == 3 && (p < c || p >= c + AD_KW)) {
       float sf = 0.f;
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
