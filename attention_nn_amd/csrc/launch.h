@@ -290,10 +290,10 @@ constexpr size_t PD_MAX_LDS = (size_t)144 * 1024; // its dynamic LDS (row buffer
 constexpr int PD_MAX_SLONG = 8;                   // attention splits per (row, head)
 constexpr int PD_MAX_G = 1024;                    // work-groups
 
-// Exchange area of the persistent decode step (up to PD_MAX_B rows), in
-// 64-bit words: tagged words of xq, xp, xm, xh, xx, xk, then the generation
-// and error words.  xm and xx hold PD_MAX_REP copies pd_rep_stride words
-// apart; xp and xh have room for PD_MAX_REP copies pd_p_stride / pd_h_stride
+// Exchange area of the persistent decode step (up to PD_MAX_B rows): 64-bit
+// tagged words of xq, xp, xm, xh, xx, xk, then the generation and error
+// words (strides in words, pd_layout offsets in bytes).  xm and xx hold
+// PD_MAX_REP copies pd_rep_stride words apart; xp and xh have room for PD_MAX_REP copies pd_p_stride / pd_h_stride
 // apart, of which the step uses PD_REP_P / PD_REP_H (the measured layout:
 // packing the areas tighter moved the step's time by up to 2.7%).  Functions
 // of d and H only, so a kernel instance with both as constants derives every
