@@ -996,15 +996,25 @@ __global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, i
     for (int j = 0; j < T; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < kw; s0 += KB) {
     uint4 ca[KB][T], cw[KB][T];
+    // every load unconditional (rows clamped in ap / wp, k-steps past the
+    // wave's range re-read its last one), so they issue back to back with
+    // no branch: a row past M or N only feeds outputs that are never stored,
+    // and k-steps past the range are zeroed once all loads are in flight
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
-      const bool ok = s0 + i < kw;
+      const int ks = min(s0 + i, kw - 1);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        ca[i][t] = (ok && aok[t]) ? *(const uint4*)(ap[t] + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
-        cw[i][t] = (ok && wok[t]) ? *(const uint4*)(wp[t] + (s0 + i) * 32) : make_uint4(0, 0, 0, 0);
+        ca[i][t] = *(const uint4*)(ap[t] + ks * 32);
+        cw[i][t] = *(const uint4*)(wp[t] + ks * 32);
       }
     }
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (s0 + i >= kw) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) ca[i][t] = cw[i][t] = make_uint4(0, 0, 0, 0);
+      }
     float scale[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) scale[t] = 1.f;
