@@ -766,18 +766,24 @@ def test_persistent_155m_late_positions_match_oracle():
     assert worst < LOGIT_TOL, worst
 
 
-@pytest.mark.parametrize("var,B", [("ANN_PD_XCD", 1), ("ANN_PD_SPECIALIZE", 1),
-                                   ("ANN_PD_SPECIALIZE", 2)])
-def test_persistent_155m_variants_bitwise(var, B, monkeypatch):
-    """The persistent step at 155M against two of its variants, teacher-forced
+@pytest.mark.parametrize("var,B,va,vb", [("ANN_PD_XCD", 1, "1", "0"),
+                                         ("ANN_PD_SPECIALIZE", 1, "1", "0"),
+                                         ("ANN_PD_SPECIALIZE", 2, "1", "0"),
+                                         ("ANN_PD_ON", 1, "96", "112"),
+                                         ("ANN_PD_REP", 1, "8", "4")])
+def test_persistent_155m_variants_bitwise(var, B, va, vb, monkeypatch):
+    """The persistent step at 155M against its variants, teacher-forced
     decode steps after a 500-token prefill (windowed layers over three splits,
     full-causal over eight at one row), logits bitwise equal:
     ANN_PD_XCD=0 splits the qkv rows contiguously over all work-groups
     instead of each head's rows and attention splits on XCD h (the default
     where the shares divide: 192 work-groups, 8 row pairs each);
     ANN_PD_SPECIALIZE=0 runs the generic kernel instead of the instance with
-    the 155M model's d and H as compile-time constants (one and two rows).
-    Every row and attention unit is computed the same way in each pair."""
+    the 155M model's d and H as compile-time constants (one and two rows);
+    ANN_PD_ON=112 spreads the 384 o-projection row pairs over 112 work-groups
+    instead of 96 (unequal shares); ANN_PD_REP=4 writes 4 copies of x' / x
+    instead of 8.  Every row and attention unit is computed the same way in
+    each pair."""
     cfg = cfg_155m()
     p = perturb_lambdas(init_params(cfg, 13, dense=True))
     tok = np.random.default_rng(131).integers(0, 50257, (B, 520))
@@ -796,7 +802,7 @@ def test_persistent_155m_variants_bitwise(var, B, monkeypatch):
         eng.check_device()
         return torch.stack(lgs)
 
-    a, b = run("1"), run("0")
+    a, b = run(va), run(vb)
     assert torch.equal(a, b), (a - b).abs().max().item()
 
 
