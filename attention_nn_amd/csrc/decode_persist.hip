@@ -333,9 +333,10 @@ __device__ __forceinline__ void pd_emit(float (*stage)[PD_RMAX], int n0, int nr,
 // reload an extra instruction in the phase that needs it; with d and H
 // constant their derived sizes and the divisions by them fold away.  155M
 // batch-1 generation (d 768, H 6): 171 -> 112 spilled scalars, 179.7 ->
-// 168.0 ms (alternating A/B, three rounds, one box).  GR: greedy without
-// fp32 logits at compile time (no z, candidate or logits stores; 170.8 ->
-// 169.6 ms on the same shape).
+// 168.0 ms (alternating A/B, three rounds, one box).  GR, the step's mode at
+// compile time: 1 greedy without fp32 logits (no z, candidate or logits
+// stores; 170.8 -> 169.6 ms on the same shape), 2 sampled without fp32 logits
+// (z and candidates stored, no argmax keys); 0 reads it from P.
 template <int DH, int BM, int UD, int DM = 0, int HM = 0, int GR = 0>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   constexpr int KU = DH / 32;       // K slices per lane per chunk (4 lanes per key)
@@ -358,9 +359,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDParams P) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = gridDim.x, g = blockIdx.x;
   const int d = DM ? DM : P.d, H = HM ? HM : P.H, d2 = d >> 1;
-  const bool greedy = GR ? true : (P.greedy != 0);
+  const bool greedy = GR ? GR == 1 : (P.greedy != 0);
   float* const logits = GR ? nullptr : P.logits;
-  uint32_t* const cand = GR ? nullptr : P.cand;
+  uint32_t* const cand = GR == 1 ? nullptr : P.cand;
   // exchange areas: with d and H constant, their offsets from xq and the
   // copy strides are compile-time constants (fewer live scalars)
   u64* const xq = P.xq;
@@ -912,7 +913,9 @@ static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool
   if constexpr (BM == 1) {
     if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
       if (!pd_areas_match(P)) return hipErrorInvalidValue;
-      if (P.greedy && !P.logits) return pd_launch<128, 1, 2, 768, 6, 1>(P, G, lds, coop, st);
+      if (!P.logits)
+        return P.greedy ? pd_launch<128, 1, 2, 768, 6, 1>(P, G, lds, coop, st)
+                        : pd_launch<128, 1, 2, 768, 6, 2>(P, G, lds, coop, st);
       return pd_launch<128, 1, 2, 768, 6>(P, G, lds, coop, st);
     }
   } else {

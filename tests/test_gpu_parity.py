@@ -712,6 +712,35 @@ def test_greedy_155m_identical_64_steps():
     assert plain == ref
 
 
+def test_sampled_155m_instance_draws(monkeypatch):
+    """The 155M batch-1 step sampling at T = 0.8 / top-k 50 without fp32
+    logits (the compile-time sampled instance, the bench's sampled batch-1
+    line): 48 draws after a 32-token prompt, the same tokens as the generic
+    kernel (ANN_PD_SPECIALIZE=0) and as the instance that also returns the
+    logits, whose draws the oracle-sampler tests check."""
+    cfg = cfg_155m()
+    p = init_params(cfg, 2, dense=True)
+    prompt = np.random.default_rng(22).integers(0, 50257, (1, 32))
+
+    def run(spec, want_logits):
+        monkeypatch.setenv("ANN_PD_SPECIALIZE", spec)
+        eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+        monkeypatch.delenv("ANN_PD_SPECIALIZE")
+        print(f"case 155M sampled, ANN_PD_SPECIALIZE={spec}, logits={want_logits}", flush=True)
+        nxt, _ = eng.prefill(prompt, 0.8, 50, 9, 0, want_logits=want_logits)
+        toks = [int(nxt.item())]
+        for i in range(47):
+            nxt, _ = eng.decode(nxt, 0.8, 50, 9, i + 1, want_logits=want_logits, out=nxt)
+            toks.append(int(nxt.item()))
+        eng.check_device()
+        return toks
+
+    inst = run("1", False)
+    assert inst == run("0", False)
+    assert inst == run("1", True)
+    assert len(set(inst)) > 8   # the draws are not one repeated token
+
+
 @pytest.mark.parametrize("B", [3, 4])
 def test_greedy_155m_rows_identical_to_oracle(B, monkeypatch):
     """The 155M model, three and four independent sequences on the
