@@ -908,21 +908,15 @@ template <int BM>
 static hipError_t pd_dispatch(const PDParams& P, int Dh, int G, size_t lds, bool coop,
                               bool spec, hipStream_t st) {
   // the 155M model's shape (d 768, H 6 x 128) at 1-4 rows: its own instances
-  // (which derive the exchange areas from xq: the caller's must match);
-  // 2 / 3 rows 245 -> 224 / 294 -> 267 us per step (positions 520-647)
-  if constexpr (BM == 1) {
-    if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
-      if (!pd_areas_match(P)) return hipErrorInvalidValue;
-      if (!P.logits)
-        return P.greedy ? pd_launch<128, 1, 2, 768, 6, 1>(P, G, lds, coop, st)
-                        : pd_launch<128, 1, 2, 768, 6, 2>(P, G, lds, coop, st);
-      return pd_launch<128, 1, 2, 768, 6>(P, G, lds, coop, st);
-    }
-  } else {
-    if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
-      if (!pd_areas_match(P)) return hipErrorInvalidValue;
-      return pd_launch<128, BM, 2, 768, 6>(P, G, lds, coop, st);
-    }
+  // (which derive the exchange areas from xq: the caller's must match), the
+  // mode constant where no fp32 logits are asked for; 2 / 3 rows 245 -> 224 /
+  // 294 -> 267 us per step (positions 520-647)
+  if (spec && Dh == 128 && P.d == 768 && P.H == 6) {
+    if (!pd_areas_match(P)) return hipErrorInvalidValue;
+    if (!P.logits)
+      return P.greedy ? pd_launch<128, BM, 2, 768, 6, 1>(P, G, lds, coop, st)
+                      : pd_launch<128, BM, 2, 768, 6, 2>(P, G, lds, coop, st);
+    return pd_launch<128, BM, 2, 768, 6>(P, G, lds, coop, st);
   }
   switch (Dh * 16 + decode_persist_slots(P.d)) {
     case 64 * 16 + 1: return pd_launch<64, BM, 1>(P, G, lds, coop, st);

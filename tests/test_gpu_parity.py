@@ -712,33 +712,40 @@ def test_greedy_155m_identical_64_steps():
     assert plain == ref
 
 
-def test_sampled_155m_instance_draws(monkeypatch):
-    """The 155M batch-1 step sampling at T = 0.8 / top-k 50 without fp32
-    logits (the compile-time sampled instance, the bench's sampled batch-1
-    line): 48 draws after a 32-token prompt, the same tokens as the generic
-    kernel (ANN_PD_SPECIALIZE=0) and as the instance that also returns the
-    logits, whose draws the oracle-sampler tests check."""
+@pytest.mark.parametrize("B,temp", [(1, 0.8), (3, 0.0), (4, 0.8)])
+def test_155m_mode_instances_draws(B, temp, monkeypatch):
+    """The 155M persistent step without fp32 logits runs instances with the
+    mode (greedy or sampled) at compile time (the bench's batch-1 lines, and
+    2-4 rows): 48 steps after 32-token prompts, greedy or T = 0.8 / top-k 50,
+    the same tokens in every row as the generic kernel (ANN_PD_SPECIALIZE=0)
+    and as the instance that also returns the logits, whose tokens and draws
+    the oracle tests check."""
     cfg = cfg_155m()
     p = init_params(cfg, 2, dense=True)
-    prompt = np.random.default_rng(22).integers(0, 50257, (1, 32))
+    prompt = np.random.default_rng(22 + B).integers(0, 50257, (B, 32))
+    k = 50 if temp > 0 else 0
 
     def run(spec, want_logits):
         monkeypatch.setenv("ANN_PD_SPECIALIZE", spec)
-        eng = _engine(cfg, p, 1, ctx=1024, tokens=1024)
+        monkeypatch.setenv("ANN_PERSIST_MAX_B", "4")
+        eng = _engine(cfg, p, B, ctx=1024, tokens=B * 32)
         monkeypatch.delenv("ANN_PD_SPECIALIZE")
-        print(f"case 155M sampled, ANN_PD_SPECIALIZE={spec}, logits={want_logits}", flush=True)
-        nxt, _ = eng.prefill(prompt, 0.8, 50, 9, 0, want_logits=want_logits)
-        toks = [int(nxt.item())]
+        monkeypatch.delenv("ANN_PERSIST_MAX_B")
+        print(f"case 155M {B} rows, T={temp}, ANN_PD_SPECIALIZE={spec}, logits={want_logits}",
+              flush=True)
+        nxt, _ = eng.prefill(prompt, temp, k, 9, 0, want_logits=want_logits)
+        toks = [nxt.cpu().numpy().copy()]
         for i in range(47):
-            nxt, _ = eng.decode(nxt, 0.8, 50, 9, i + 1, want_logits=want_logits, out=nxt)
-            toks.append(int(nxt.item()))
+            nxt, _ = eng.decode(nxt, temp, k, 9, i + 1, want_logits=want_logits, out=nxt)
+            toks.append(nxt.cpu().numpy().copy())
         eng.check_device()
-        return toks
+        return np.stack(toks)
 
     inst = run("1", False)
-    assert inst == run("0", False)
-    assert inst == run("1", True)
-    assert len(set(inst)) > 8   # the draws are not one repeated token
+    assert np.array_equal(inst, run("0", False))
+    assert np.array_equal(inst, run("1", True))
+    if temp > 0:   # the draws are not one repeated token (greedy at this init can be)
+        assert len(set(inst[:, 0].tolist())) > 8
 
 
 @pytest.mark.parametrize("B", [3, 4])
