@@ -296,33 +296,58 @@ __global__ void k_relu2(const T* __restrict__ x, T* __restrict__ y, size_t n) {
   }
 }
 
-// rope_ht (metal_kernels.py:87-113), one thread per dim pair, explicit pos0.
-template <typename T>
-__global__ void k_rope(const T* __restrict__ x, T* __restrict__ y, const float* __restrict__ cs,
-                       const float* __restrict__ sn, int B, int Tn, int H, int D, int pos0,
-                       int inverse) {
-  const size_t n = (size_t)B * Tn * H * (D / 2);
-  size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= n) return;
-  const int D2 = D / 2, D4 = D / 4;
-  size_t row = p / ((size_t)H * D2);
-  int rem = (int)(p % ((size_t)H * D2));
-  int h = rem / D2, d2 = rem % D2;
-  int t = (int)(row % Tn) + pos0;
-  size_t base = row * (size_t)(H * D) + (size_t)h * D + 2 * d2;
-  float x0 = ldf(x, base), x1 = ldf(x, base + 1);
-  if (d2 < D4) {
-    float c = cs[(size_t)t * D4 + d2], s = sn[(size_t)t * D4 + d2];
-    if (inverse) {
-      stf(y, base, c * x0 - s * x1);
-      stf(y, base + 1, c * x1 + s * x0);
+// rope_ht (metal_kernels.py:87-134 semantics): each head vector of D elements
+// is rotated in adjacent pairs, pair j < D/4 by the angle of table index j at
+// position pos0 + t, pairs j >= D/4 passed through.  One wave per (row, head)
+// vector, four vectors per 256-thread work-group; lane l moves pairs l,
+// l + 64, ..  (as one 8-byte / 4-byte word where x and y allow, VEC).  The
+// inverse rotation is the forward one with the sine negated.
+template <typename T> struct RopePair;
+template <> struct RopePair<float> {
+  typedef float2 W;
+  static __device__ __forceinline__ void get(W w, float& a, float& b) { a = w.x; b = w.y; }
+  static __device__ __forceinline__ W put(float a, float b) { return make_float2(a, b); }
+};
+template <> struct RopePair<bf16_t> {
+  typedef uint32_t W;
+  static __device__ __forceinline__ void get(W w, float& a, float& b) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ W put(float a, float b) { return pack2(a, b); }
+};
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void k_rope(const T* __restrict__ x, T* __restrict__ y,
+                                              const float* __restrict__ cs,
+                                              const float* __restrict__ sn, long long nvec, int Tn,
+                                              int H, int D, int pos0, float sgn) {
+  const long long v = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= nvec) return;
+  const int lane = threadIdx.x & 63, nrot = D / 4;
+  const size_t tab = (size_t)((int)((v / H) % Tn) + pos0) * nrot;
+  const T* xv = x + (size_t)v * D;
+  T* yv = y + (size_t)v * D;
+  for (int j = lane; j < D / 2; j += 64) {
+    float a, b;
+    if constexpr (VEC) {
+      RopePair<T>::get(((const typename RopePair<T>::W*)xv)[j], a, b);
     } else {
-      stf(y, base, c * x0 + s * x1);
-      stf(y, base + 1, c * x1 - s * x0);
+      a = ldf(xv, 2 * j);
+      b = ldf(xv, 2 * j + 1);
     }
-  } else {
-    stf(y, base, x0);
-    stf(y, base + 1, x1);
+    if (j < nrot) {
+      const float c = cs[tab + j], s = sgn * sn[tab + j];
+      const float ra = c * a + s * b, rb = c * b - s * a;
+      a = ra;
+      b = rb;
+    }
+    if constexpr (VEC) {
+      ((typename RopePair<T>::W*)yv)[j] = RopePair<T>::put(a, b);
+    } else {
+      stf(yv, 2 * j, a);
+      stf(yv, 2 * j + 1, b);
+    }
   }
 }
 
@@ -437,14 +462,22 @@ hipError_t op_relu2(const void* x, void* y, size_t n, int dtype, hipStream_t st)
 
 hipError_t op_rope(const void* x, void* y, const float* cs, const float* sn, int B, int T, int H,
                    int D, int pos0, int inverse, int dtype, hipStream_t st) {
-  size_t n = (size_t)B * T * H * (D / 2);
-  if (n == 0) return hipSuccess;
-  if (dtype == 0)
-    hipLaunchKernelGGL(k_rope<float>, dim3(cdiv(n, 256)), dim3(256), 0, st, (const float*)x,
-                       (float*)y, cs, sn, B, T, H, D, pos0, inverse);
-  else
-    hipLaunchKernelGGL(k_rope<bf16_t>, dim3(cdiv(n, 256)), dim3(256), 0, st, (const bf16_t*)x,
-                       (bf16_t*)y, cs, sn, B, T, H, D, pos0, inverse);
+  const long long nvec = (long long)B * T * H;
+  if (nvec == 0) return hipSuccess;
+  const dim3 grid((unsigned)((nvec + 3) / 4));
+  const float sgn = inverse ? -1.f : 1.f;
+  // pairs as whole words when both buffers are aligned to a pair
+  const uintptr_t pa = (dtype == 0 ? 8 : 4) - 1;
+  const bool vec = (((uintptr_t)x | (uintptr_t)y) & pa) == 0;
+#define ANN_ROPE(TY, V)                                                                       \
+  hipLaunchKernelGGL((k_rope<TY, V>), grid, dim3(256), 0, st, (const TY*)x, (TY*)y, cs, sn, nvec, \
+                     T, H, D, pos0, sgn)
+  if (dtype == 0) {
+    if (vec) ANN_ROPE(float, true); else ANN_ROPE(float, false);
+  } else {
+    if (vec) ANN_ROPE(bf16_t, true); else ANN_ROPE(bf16_t, false);
+  }
+#undef ANN_ROPE
   return hipGetLastError();
 }
 

@@ -75,7 +75,17 @@ def test_rope_kernel_kat():
     a = K.rope_ht(torch.from_numpy(x).cuda(), cs2, sn2, pos0=20).cpu().numpy()
     r = _rope_reference_loop(x, cs2.cpu().numpy()[20:36], sn2.cpu().numpy()[20:36])
     assert np.allclose(a, r, atol=1e-5)
-    assert K.rope_ht(torch.from_numpy(x).cuda().bfloat16(), cs, sn).dtype == torch.bfloat16
+    xb = torch.from_numpy(x).cuda().bfloat16()
+    yb = K.rope_ht(xb, cs, sn)
+    assert yb.dtype == torch.bfloat16
+    rb = _rope_reference_loop(xb.float().cpu().numpy(), cs.cpu().numpy(), sn.cpu().numpy())
+    rb = torch.from_numpy(rb).bfloat16().float().numpy()   # the fp32 rotation rounded once
+    assert np.allclose(yb.float().cpu().numpy(), rb, rtol=2 ** -7, atol=1e-6)
+    # buffers one element off a pair boundary: the element-wise path of the kernel
+    big = torch.zeros(x.size + 1, dtype=torch.float32, device="cuda")
+    xo = big[1:].view(x.shape)
+    xo.copy_(torch.from_numpy(x).cuda())
+    assert np.allclose(K.rope_ht(xo, cs, sn).cpu().numpy(), ref, atol=1e-5)
 
 
 def test_rope_tables_long():
