@@ -816,7 +816,8 @@ def test_persistent_155m_late_positions_match_oracle():
                                          ("ANN_PD_SPECIALIZE", 1, "1", "0"),
                                          ("ANN_PD_SPECIALIZE", 2, "1", "0"),
                                          ("ANN_PD_ON", 1, "96", "112"),
-                                         ("ANN_PD_REP", 1, "8", "4")])
+                                         ("ANN_PD_REP", 1, "8", "4"),
+                                         ("ANN_PERSIST_G", 1, "192", "128")])
 def test_persistent_155m_variants_bitwise(var, B, va, vb, monkeypatch):
     """The persistent step at 155M against its variants, teacher-forced
     decode steps after a 500-token prefill (windowed layers over three splits,
@@ -828,8 +829,9 @@ def test_persistent_155m_variants_bitwise(var, B, va, vb, monkeypatch):
     the 155M model's d and H as compile-time constants (one and two rows);
     ANN_PD_ON=112 spreads the 384 o-projection row pairs over 112 work-groups
     instead of 96 (unequal shares); ANN_PD_REP=4 writes 4 copies of x' / x
-    instead of 8.  Every row and attention unit is computed the same way in
-    each pair."""
+    instead of 8; ANN_PERSIST_G=128 runs the step on 128 work-groups instead
+    of 192 (other row shares, the contiguous qkv layout).  Every row and
+    attention unit is computed the same way in each pair."""
     cfg = cfg_155m()
     p = perturb_lambdas(init_params(cfg, 13, dense=True))
     tok = np.random.default_rng(131).integers(0, 50257, (B, 520))
