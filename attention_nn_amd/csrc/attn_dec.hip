@@ -40,6 +40,7 @@
 #include <stdlib.h>
 #include "common.h"
 #include "launch.h"
+#include "sk_gemm.h"
 
 namespace ann {
 
@@ -83,24 +84,15 @@ __device__ __forceinline__ void weight_prefetch(const uint4* __restrict__ p, siz
   if (f == AD_PF_MAGIC) *sink = f;
 }
 
-// RING chunks in flight per wave.  RING 3 takes 195 VGPRs (two work-groups
-// per CU); RING 2 is held to 128 (four per CU) for grids of many (b, h)
-// work-groups, which then run in fewer rounds.
-template <int DH, int RING>
-__global__ __launch_bounds__(AD_THREADS) __attribute__((amdgpu_waves_per_eu(RING == 2 ? 3 : 1)))
-void k_attn_dec(
-    const bf16_t* __restrict__ qkv, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+// The attention of work-group (split, h, b); qkv_src(b, h, t, q, k, v) gives
+// lane t's pair of the new token's raw q, k and v.
+template <int DH, int RING, typename QKV>
+__device__ __forceinline__ void attn_dec_body(
+    QKV&& qkv_src, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
     u64* __restrict__ part, unsigned* __restrict__ cnt, unsigned* __restrict__ err,
     bf16_t* __restrict__ out, int H, int max_ctx, int window, int is_long, float scale, float shift,
-    float eps, int nsplit, int nb, const uint4* __restrict__ pf, size_t pf_n16,
-    unsigned long long* __restrict__ pf_sink) {
-  if ((int)blockIdx.z >= nb) {   // grid.z slices past the batch: weight prefetch only
-    const unsigned P = (gridDim.z - nb) * gridDim.y * gridDim.x;
-    const unsigned wg = ((blockIdx.z - nb) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-    weight_prefetch(pf, pf_n16, wg, P, pf_sink);
-    return;
-  }
+    float eps, int nsplit, int split, int h, int b) {
   constexpr int KU = DH / 32;       // 16-byte K slices per lane per chunk (4 lanes per key)
   constexpr int VL = DH / 8;        // lanes per V row
   constexpr int VP = 64 / VL;       // V rows per pass of the wave
@@ -113,7 +105,6 @@ void k_attn_dec(
   __shared__ float s_o[AD_THREADS / 64][DH];
   __shared__ float s_l[AD_THREADS / 64];
 
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   // the wave index as a scalar (the per-chunk test below is uniform)
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // the ticket is taken first; its value is read after the barriers below
@@ -159,10 +150,8 @@ void k_attn_dec(
 
   // ---- new token: QK-norm + RoPE (wave 0, one dim pair per lane)
   if (tid < P) {
-    const bf16_t* row = qkv + (size_t)b * 3 * d + h * DH + 2 * tid;
-    const uint32_t qw = *(const uint32_t*)row;
-    const uint32_t kw = *(const uint32_t*)(row + d);
-    const uint32_t vw = *(const uint32_t*)(row + 2 * d);
+    uint32_t qw, kw, vw;   // this lane's q, k, v pair of the new token
+    qkv_src(b, h, tid, qw, kw, vw);
     float q0 = __uint_as_float(qw << 16), q1 = __uint_as_float(qw & 0xffff0000u);
     float c0 = __uint_as_float(kw << 16), c1 = __uint_as_float(kw & 0xffff0000u);
     const float sq = group_sum<P>(q0 * q0 + q1 * q1);
@@ -337,6 +326,130 @@ void k_attn_dec(
     }
     out[(size_t)b * d + h * DH + tid] = f2bf(o / l);
   }
+}
+
+// RING chunks in flight per wave.  RING 3 takes 195 VGPRs (two work-groups
+// per CU); RING 2 is held to 128 (four per CU) for grids of many (b, h)
+// work-groups, which then run in fewer rounds.
+template <int DH, int RING>
+__global__ __launch_bounds__(AD_THREADS) __attribute__((amdgpu_waves_per_eu(RING == 2 ? 3 : 1)))
+void k_attn_dec(
+    const bf16_t* __restrict__ qkv, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+    const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
+    u64* __restrict__ part, unsigned* __restrict__ cnt, unsigned* __restrict__ err,
+    bf16_t* __restrict__ out, int H, int max_ctx, int window, int is_long, float scale, float shift,
+    float eps, int nsplit, int nb, const uint4* __restrict__ pf, size_t pf_n16,
+    unsigned long long* __restrict__ pf_sink) {
+  if ((int)blockIdx.z >= nb) {   // grid.z slices past the batch: weight prefetch only
+    const unsigned P = (gridDim.z - nb) * gridDim.y * gridDim.x;
+    const unsigned wg = ((blockIdx.z - nb) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    weight_prefetch(pf, pf_n16, wg, P, pf_sink);
+    return;
+  }
+  const int d = H * DH;
+  attn_dec_body<DH, RING>(
+      [&](int b, int h, int t, uint32_t& qw, uint32_t& kw, uint32_t& vw) {
+        const bf16_t* row = qkv + (size_t)b * 3 * d + h * DH + 2 * t;
+        qw = *(const uint32_t*)row;
+        kw = *(const uint32_t*)(row + d);
+        vw = *(const uint32_t*)(row + 2 * d);
+      },
+      kc, vc, pos, cs, sn, part, cnt, err, out, H, max_ctx, window, is_long, scale, shift, eps,
+      nsplit, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// The decode step's RMS + qkv projection and its attention in one launch
+// (batch 16..64, d <= 768, direct launches only): work-groups [0, ngemm) run
+// the skinny GEMM's 16T x 16T tiles (gemm_sk_body, the same arithmetic as
+// k_gemm_sk) and publish bf16 pairs of q, k, v as tagged words xt[m][n / 2]
+// (tag = this launch's, from a host counter that only grows); the attention
+// work-groups after them (then the weight-prefetch ones) issue their first
+// K/V chunks and wait for their (b, h)'s words, so the cache streaming and the
+// projection overlap and one launch boundary goes.  Work-groups are
+// dispatched in index order, so the projection tiles are resident before any
+// attention work-group waits; every wait is bounded.
+template <int DH, int RING, int T>
+__global__ __launch_bounds__(AD_THREADS) __attribute__((amdgpu_waves_per_eu(RING == 2 ? 3 : 1)))
+void k_qkv_attn_dec(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wqkv, int ngemm, int gx,
+    u64* __restrict__ xt, uint32_t tag, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+    const int32_t* __restrict__ pos, const float* __restrict__ cs, const float* __restrict__ sn,
+    u64* __restrict__ part, unsigned* __restrict__ cnt, unsigned* __restrict__ err,
+    bf16_t* __restrict__ out, int H, int max_ctx, int window, int is_long, float scale, float shift,
+    float eps, int nsplit, int nb, const uint4* __restrict__ pf, size_t pf_n16,
+    unsigned long long* __restrict__ pf_sink) {
+  const int d = H * DH, d2 = d / 2, L = blockIdx.x;
+  if (L < ngemm) {
+    gemm_sk_body<true, 6, T>(x, d, wqkv, nb, 3 * d, d, eps, L % gx, L / gx,
+                             [&](int m, int n, const sk_floatx4_t& v) {
+                               float vn[4];
+#pragma unroll
+                               for (int r = 0; r < 4; ++r) vn[r] = __shfl_down(v[r], 1, 64);
+                               if (n & 1) return;
+#pragma unroll
+                               for (int r = 0; r < 4; ++r)
+                                 if (m + r < nb)
+                                   ll_store(xt + (size_t)(m + r) * 3 * d2 + (n >> 1),
+                                            pack2(v[r], vn[r]), tag);
+                             });
+    return;
+  }
+  const int a = L - ngemm, per = nsplit * H;
+  if (a >= nb * per) {   // weight prefetch
+    weight_prefetch(pf, pf_n16, a - nb * per, gridDim.x - ngemm - nb * per, pf_sink);
+    return;
+  }
+  attn_dec_body<DH, RING>(
+      [&](int b, int h, int t, uint32_t& qw, uint32_t& kw, uint32_t& vw) {
+        const u64* w = xt + (size_t)b * 3 * d2 + h * (DH / 2) + t;
+        qw = ll_wait(w, tag, err);
+        kw = ll_wait(w + d2, tag, err);
+        vw = ll_wait(w + d, tag, err);
+      },
+      kc, vc, pos, cs, sn, part, cnt, err, out, H, max_ctx, window, is_long, scale, shift, eps,
+      nsplit, a % nsplit, (a / nsplit) % H, a / per);
+}
+
+hipError_t qkv_attn_decode(const bf16_t* x, const bf16_t* wqkv, u64* xt, uint32_t tag,
+                           bf16_t* kc, bf16_t* vc, const int32_t* pos, const float* cs,
+                           const float* sn, u64* part, unsigned* cnt, unsigned* err, bf16_t* out,
+                           int B, int H, int Dh, int max_ctx, int window, bool long_layer,
+                           float scale, float eps, int nsplit, const WeightPrefetch& pf,
+                           hipStream_t st) {
+  const int d = H * Dh;
+  if (!qkv_attn_fits(B, d, Dh) || nsplit < 1 || nsplit > AD_MAX_SPLIT) return hipErrorInvalidValue;
+  const bool pfon = pf.slices > 0 && pf.bytes >= 16 && pf.p && pf.sink;
+  if (pfon && ((uintptr_t)pf.p & 15)) return hipErrorInvalidValue;
+  const float shift = scale * (float)Dh * 1.02f;
+  // the skinny GEMM's tile choice for these shapes (gemm_skinny): 32 x 32
+  // tiles above 32 rows (N = 3d >= 2048 here), else 16 x 16
+  const int T = B > 32 ? 2 : 1;
+  const int gx = (3 * d + 16 * T - 1) / (16 * T), gy = (B + 16 * T - 1) / (16 * T);
+  const int ngemm = gx * gy;
+  const int natt = nsplit * H * (B + (pfon ? pf.slices : 0));
+  const uint4* pfp = pfon ? (const uint4*)pf.p : nullptr;
+  const size_t pfn = pfon ? pf.bytes / 16 : 0;
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  const bool r2 = (long long)nsplit * H * B > 2LL * cus;
+#define ANN_QA(R, TT)                                                                          \
+  hipLaunchKernelGGL((k_qkv_attn_dec<128, R, TT>), dim3(ngemm + natt), dim3(AD_THREADS), 0, st, \
+                     x, wqkv, ngemm, gx, xt, tag, kc, vc, pos, cs, sn, part, cnt, err, out, H,  \
+                     max_ctx, window, (int)long_layer, scale, shift, eps, nsplit, B, pfp, pfn,  \
+                     pf.sink)
+  if (T == 2) {
+    if (r2) ANN_QA(2, 2); else ANN_QA(3, 2);
+  } else {
+    if (r2) ANN_QA(2, 1); else ANN_QA(3, 1);
+  }
+#undef ANN_QA
+  return hipGetLastError();
 }
 
 hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t* pos,

@@ -75,6 +75,7 @@ WLayout weight_layout(const ann_config& c) {
 
 struct SLayout {  // byte offsets into the workspace
   size_t pos, sp, steps, amax, acnt, pfsink, x, x0, qkv, q, ao, hn, hid, part, zb, pcand, pd,
+      qat,
       pd_bytes,
       ce, ce_tz, ce_rows, ce_mean, total;
 };
@@ -96,6 +97,7 @@ SLayout ws_layout(const ann_config& c) {
   s.amax = off; off += up((B <= 8 ? B : 1) * (size_t)gemv_blocks(c.V, c.d) * 8);
   s.acnt = off; off += up(B * c.H * 4);
   s.pfsink = off; off += up(8);
+  s.qat = off; off += up((size_t)c.max_batch * 3 * c.d / 2 * 8);   // fused qkv -> attention words
   s.x = off; off += up(M * d * 2);
   s.x0 = off; off += up(M * d * 2);
   s.qkv = off; off += up(M * 3 * d * 2);
@@ -198,6 +200,8 @@ struct ann_ctx {
   // the next projections' weights ahead; -1 = not read yet, -2 = sized by
   // bytes, >= 0 = fixed by ANN_PREFETCH_WG
   int pf_wgs = -1;
+  bool qa_env = true;      // ANN_QKV_ATTN: the fused qkv projection + decode attention
+  uint32_t qa_tag = 0;     // tag of its last launch (0: none since the decode state was cleared)
   // decode attention: splits per (row, head) fixed by ANN_DEC_SPLITS (0: sized
   // by the batch, about 384 work-groups)
   int dec_split_env = 0;
@@ -340,6 +344,8 @@ int clear_decode_state(ann_ctx* c, hipStream_t st) {
   HIPCHK(hipMemsetAsync(c->ws + c->sl.acnt, 0, (size_t)g.max_batch * g.H * 4, st));
   HIPCHK(hipMemsetAsync(c->ws + c->sl.part, 0,
                         (size_t)g.max_batch * g.H * MAX_SPLIT * (c->Dh + 1) * 8, st));
+  HIPCHK(hipMemsetAsync(c->ws + c->sl.qat, 0, (size_t)g.max_batch * 3 * g.d / 2 * 8, st));
+  c->qa_tag = 0;
   c->dec_clear = false;
   return ANN_OK;
 }
@@ -395,9 +401,21 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
         fuse_qkv = true;
       }
     }
-    int rc = proj(c, ANN_PROF_QKV, fuse_qkv ? EPI_QKV : EPI_STORE, PRE_RMS,
-                  c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d, ea, st);
-    if (rc) return rc;
+    // decode of 16..64 rows launched directly: the qkv projection and the
+    // attention as one launch (qkv_attn_decode); never inside a graph
+    // capture (its tag comes from a host counter) or a per-kernel profile
+    bool fuse_qa = T == 1 && c->qa_env && c->prof_kind < 0 && qkv_attn_fits(B, d, Dh);
+    if (fuse_qa) {
+      hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+      HIPCHK(hipStreamIsCapturing(st, &cst));
+      fuse_qa = cst == hipStreamCaptureStatusNone;
+    }
+    int rc = ANN_OK;
+    if (!fuse_qa) {
+      rc = proj(c, ANN_PROF_QKV, fuse_qkv ? EPI_QKV : EPI_STORE, PRE_RMS,
+                c->layer_w(l, c->wl.qkv), x, d, M, 3 * d, d, ea, st);
+      if (rc) return rc;
+    }
     EpiArgs er{};
     er.x = x;
     er.x0 = x0;
@@ -417,7 +435,13 @@ int run_body(ann_ctx* c, const int32_t* tokens, int B, int T, hipStream_t st) {
         pf.slices = (pfw + ns * H - 1) / (ns * H);
         pf.sink = c->sp<unsigned long long>(c->sl.pfsink);
       }
-      {
+      if (fuse_qa) {
+        c->qa_tag += 1;
+        HIPCHK(qkv_attn_decode(x, c->layer_w(l, c->wl.qkv), c->sp<u64>(c->sl.qat), c->qa_tag,
+                               c->kcache(l), c->vcache(l), pos, cs, sn, part,
+                               c->sp<unsigned>(c->sl.acnt), err, ao, B, H, Dh, g.max_ctx,
+                               g.window, lng, g.attn_scale, g.rms_eps, ns, pf, st));
+      } else {
         ProfScope ps(c, ANN_PROF_ATTN, st);
         HIPCHK(attn_decode(qkv, c->kcache(l), c->vcache(l), pos, cs, sn, part,
                            c->sp<unsigned>(c->sl.acnt), err, ao, B, H, Dh, g.max_ctx, g.window, lng,
@@ -781,6 +805,8 @@ int ann_create(const ann_config* cfg, ann_ctx** out) {
   c->cand_env = !(tc && tc[0] == '0');
   const char* tv = getenv("ANN_TOPK_VERIFY");
   c->cand_verify = tv && tv[0] == '1';
+  const char* qa = getenv("ANN_QKV_ATTN");
+  c->qa_env = !(qa && qa[0] == '0');
   const char* pc = getenv("ANN_PERSIST_COOP");
   c->pd_coop = pc && pc[0] == '1';
   *out = c;

@@ -199,6 +199,19 @@ hipError_t attn_decode(const bf16_t* qkv, bf16_t* kc, bf16_t* vc, const int32_t*
                        bf16_t* out,
                        int B, int H, int Dh, int max_ctx, int window, bool long_layer, float scale,
                        float eps, int nsplit, const WeightPrefetch& pf, hipStream_t st);
+// The decode step's RMS + qkv projection (x (B, d) against wqkv (3d, d)) and
+// the attention above in one launch: q, k, v handed over as tagged words in
+// xt (B x 3d/2 words; `tag` larger than any earlier launch's on that buffer).
+// Shapes it takes: 16..64 rows, Dh 128, d a multiple of 128 up to 768.
+constexpr bool qkv_attn_fits(int B, int d, int Dh) {
+  return B >= 16 && B <= 64 && Dh == 128 && d % 128 == 0 && d <= 768;
+}
+hipError_t qkv_attn_decode(const bf16_t* x, const bf16_t* wqkv, u64* xt, uint32_t tag,
+                           bf16_t* kc, bf16_t* vc, const int32_t* pos, const float* cs,
+                           const float* sn, u64* part, unsigned* cnt, unsigned* err, bf16_t* out,
+                           int B, int H, int Dh, int max_ctx, int window, bool long_layer,
+                           float scale, float eps, int nsplit, const WeightPrefetch& pf,
+                           hipStream_t st);
 
 // Sampling of B rows of bf16 z (B, ldz) over the first Vs entries with the
 // device-resident parameters; uses and increments steps[b]; advances pos[b]

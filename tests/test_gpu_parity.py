@@ -854,6 +854,34 @@ def test_persistent_155m_variants_bitwise(var, B, va, vb, monkeypatch):
     assert torch.equal(a, b), (a - b).abs().max().item()
 
 
+@pytest.mark.parametrize("B", [16, 33, 64])
+def test_fused_qkv_attention_bitwise(B, monkeypatch):
+    """Decode steps of 16..64 rows (155M) with the qkv projection and the
+    attention in one launch (tagged q / k / v words) against the two separate
+    launches (ANN_QKV_ATTN=0): teacher-forced steps after a 300-token prefill,
+    windowed and full-causal layers, logits bitwise equal."""
+    cfg = cfg_155m()
+    p = perturb_lambdas(init_params(cfg, 17, dense=True))
+    tok = np.random.default_rng(170 + B).integers(0, 50257, (B, 312))
+
+    def run(val):
+        monkeypatch.setenv("ANN_QKV_ATTN", val)
+        eng = _engine(cfg, p, B, ctx=1024, tokens=B * 300)
+        monkeypatch.delenv("ANN_QKV_ATTN")
+        print(f"case 155M {B} rows, ANN_QKV_ATTN={val}: prefill 300, 12 decode steps", flush=True)
+        eng.prefill(tok[:, :300])
+        lgs = []
+        for i in range(300, 312):
+            t = torch.from_numpy(tok[:, i].astype(np.int32)).cuda()
+            _, lg = eng.decode(t, want_logits=True)
+            lgs.append(lg.cpu())
+        eng.check_device()
+        return torch.stack(lgs)
+
+    a, b = run("1"), run("0")
+    assert torch.equal(a, b), (a - b).abs().max().item()
+
+
 def test_degenerate_init_repeats_last_token():
     """cfg1 as specified (model.py init: Wo = proj = x0 = 0): greedy repeats
     the last prompt token; logits equal the oracle's closed form."""
